@@ -1,0 +1,59 @@
+/*
+ * kernel-set (MI355X build) -- quantized GEMMs.
+ *
+ * The three entry points keep the exact prototypes of the reference ABI
+ * (include/kernel_set/gemm.h of cklxx/kernel-set) so existing bindings load
+ * this library unchanged. All matrices are row-major and device resident;
+ * every call only enqueues work on `stream` (NULL = null stream).
+ *
+ * Out of scope for this build (not exported): ks_gemm, ks_gemm_bias_act,
+ * ks_gemm_batched, ks_gemm_fp8 (per-token), ks_gemm_nvfp4.
+ */
+#ifndef KERNEL_SET_GEMM_H_
+#define KERNEL_SET_GEMM_H_
+
+#include "kernel_set/types.h"
+
+KS_BEGIN_EXTERN_C
+
+/* Replaces reference gemm.h:39-49 (kernels/src/gemm/gemm_w8a8.cu:166-217).
+ * C[M,N] = (float(acc) * a_s) * b_s (+ bias), acc = sum_k A[m,k]*B[k,n] in exact
+ * int32. A int8 [M,K], B int8 [K,N]. a_scale fp32 [M] (PER_TOKEN) or [1]
+ * (PER_TENSOR); b_scale fp32 [N] (PER_CHANNEL) or [1] (PER_TENSOR). bias is [N]
+ * in out_dtype or NULL. out_dtype f32/f16/bf16. Runs on int8 MFMA. */
+KS_API ks_status_t ks_gemm_w8a8(void* c, const void* a_i8, const void* b_i8,
+                                const float* a_scale, const float* b_scale,
+                                const void* bias, int64_t m, int64_t n,
+                                int64_t k, ks_quant_mode_t a_mode,
+                                ks_quant_mode_t b_mode, ks_dtype_t out_dtype,
+                                ks_stream_t stream);
+
+/* Replaces reference gemm.h:51-59 (kernels/src/gemm/gemm_w4a16.cu:151-182).
+ * C[M,N] = A[M,K] @ W + bias, W[k,n] = (q[k,n] - zeros[k/gs,n]) * scales[k/gs,n].
+ * b_packed uint8 [K/2, N]: byte (k/2)*N+n holds q[k even] in bits 0-3 and
+ * q[k odd] in bits 4-7, codes 0..15. scales/zeros/bias/A/C share `dtype`
+ * (f16 or bf16); zeros and bias may be NULL (zero). group_size <= 0 means one
+ * group over all K. K must be even and a multiple of the group size. */
+KS_API ks_status_t ks_gemm_w4a16(void* c, const void* a, const void* b_packed,
+                                 const void* scales, const void* zeros,
+                                 const void* bias, int64_t m, int64_t n,
+                                 int64_t k, int group_size, ks_dtype_t dtype,
+                                 ks_stream_t stream);
+
+/* Replaces reference gemm.h:79-98 (kernels/src/gemm/gemm_fp8_blockwise.cu:218-302).
+ * fp8 A [M,K] x fp8 B [K,N] with a_scale fp32 [M, ceil(K/block_k)] and b_scale
+ * fp32 [ceil(K/block_k), ceil(N/block_n)]. For every K-block the fp32 partial
+ * sum is promoted into the output accumulator as part * (a_s * b_s). fp8_dtype
+ * is e4m3 or e5m2; out_dtype f32/f16/bf16. */
+KS_API ks_status_t ks_gemm_fp8_blockwise(void* out, const void* a_fp8,
+                                         const void* b_fp8,
+                                         const float* a_scale,
+                                         const float* b_scale, int64_t m,
+                                         int64_t n, int64_t k, int block_n,
+                                         int block_k, ks_dtype_t fp8_dtype,
+                                         ks_dtype_t out_dtype,
+                                         ks_stream_t stream);
+
+KS_END_EXTERN_C
+
+#endif /* KERNEL_SET_GEMM_H_ */

@@ -1,0 +1,24 @@
+/*
+ * kernel-set (MI355X build) -- test hooks. NOT part of the reference ABI.
+ *
+ * These exist so parity tests can check intermediate values that the public
+ * entry points never expose.
+ */
+#ifndef KERNEL_SET_TESTING_H_
+#define KERNEL_SET_TESTING_H_
+
+#include "kernel_set/types.h"
+
+KS_BEGIN_EXTERN_C
+
+/* The int32 accumulators of ks_gemm_w8a8 before any scaling:
+ * acc[M,N] = sum_k A[m,k] * B[k,n], computed by the same MFMA kernel. No
+ * reference counterpart; used to check that accumulation is exact. */
+KS_API ks_status_t ks_testing_gemm_w8a8_i32(int32_t* acc, const void* a_i8,
+                                            const void* b_i8, int64_t m,
+                                            int64_t n, int64_t k,
+                                            ks_stream_t stream);
+
+KS_END_EXTERN_C
+
+#endif /* KERNEL_SET_TESTING_H_ */

@@ -1,0 +1,248 @@
+// kernel-set (MI355X build) -- shared host/device helpers for every HIP source.
+//
+// Contents:
+//   * status/error plumbing behind ks_last_error_string (same message
+//     conventions as the reference: "null arg: <name>", "<func>: <hip msg>",
+//     kernels/src/common/dispatch.cuh:23-50 of cklxx/kernel-set);
+//   * element load/store for f32 / f16 / bf16 with round-to-nearest-even;
+//   * OCP fp8 (e4m3fn, e5m2) encode with saturation to the finite maximum and
+//     decode, written from the OCP 8-bit floating point specification;
+//   * wave64 reductions.
+// Everything here is gfx950-only: wave size 64 is assumed, not queried.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "kernel_set/types.h"
+
+namespace ks {
+
+// ---------------------------------------------------------------------------
+// Error plumbing (host)
+// ---------------------------------------------------------------------------
+void set_last_error(const std::string& msg);
+
+inline ks_status_t check_hip(hipError_t e, const char* where) {
+  if (e == hipSuccess) return KS_SUCCESS;
+  set_last_error(std::string(where) + ": " + hipGetErrorString(e));
+  return KS_ERROR_CUDA;
+}
+
+inline hipStream_t to_stream(ks_stream_t s) {
+  return reinterpret_cast<hipStream_t>(s);
+}
+
+}  // namespace ks
+
+#define KS_FAIL(status, msg)       \
+  do {                             \
+    ::ks::set_last_error(msg);     \
+    return (status);               \
+  } while (0)
+
+#define KS_REQUIRE_PTR(p)                                          \
+  do {                                                             \
+    if ((p) == nullptr)                                            \
+      KS_FAIL(KS_ERROR_INVALID_ARGUMENT, "null arg: " #p);         \
+  } while (0)
+
+// After a launch: report a launch error as KS_ERROR_CUDA "<func>: <msg>".
+#define KS_LAUNCH_STATUS(func)                                              \
+  do {                                                                      \
+    ks_status_t _st = ::ks::check_hip(hipGetLastError(), func);             \
+    if (_st != KS_SUCCESS) return _st;                                      \
+  } while (0)
+
+namespace ks {
+
+constexpr int kWave = 64;
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming load: marked non-temporal so single-use weight bytes do not
+// evict data that is reused (activations, scales, partials).
+__device__ inline uint4 load_stream16(const void* p) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+// ---------------------------------------------------------------------------
+// 16-bit float storage. Values are carried as raw uint16_t bits so one kernel
+// template serves f16 and bf16; the tag types below pick the conversion.
+// ---------------------------------------------------------------------------
+struct f32_t {
+  using storage = float;
+};
+struct f16_t {
+  using storage = uint16_t;
+};
+struct bf16_t {
+  using storage = uint16_t;
+};
+
+__device__ inline float bf16_bits_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// fp32 -> bf16, round to nearest even; NaN stays a quiet NaN.
+__device__ inline uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x0040u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ inline float f16_bits_to_f32(uint16_t h) {
+  _Float16 v;
+  __builtin_memcpy(&v, &h, 2);
+  return static_cast<float>(v);
+}
+
+__device__ inline uint16_t f32_to_f16_bits(float f) {
+  _Float16 v = static_cast<_Float16>(f);  // v_cvt_f16_f32: round to nearest even
+  uint16_t h;
+  __builtin_memcpy(&h, &v, 2);
+  return h;
+}
+
+template <typename T>
+struct elem;
+
+template <>
+struct elem<f32_t> {
+  static constexpr int bytes = 4;
+  __device__ static inline float load(const float* p, int64_t i) { return p[i]; }
+  __device__ static inline float to_f32(float v) { return v; }
+  __device__ static inline float from_f32(float v) { return v; }
+};
+
+template <>
+struct elem<f16_t> {
+  static constexpr int bytes = 2;
+  __device__ static inline float load(const uint16_t* p, int64_t i) {
+    return f16_bits_to_f32(p[i]);
+  }
+  __device__ static inline float to_f32(uint16_t v) { return f16_bits_to_f32(v); }
+  __device__ static inline uint16_t from_f32(float v) { return f32_to_f16_bits(v); }
+};
+
+template <>
+struct elem<bf16_t> {
+  static constexpr int bytes = 2;
+  __device__ static inline float load(const uint16_t* p, int64_t i) {
+    return bf16_bits_to_f32(p[i]);
+  }
+  __device__ static inline float to_f32(uint16_t v) { return bf16_bits_to_f32(v); }
+  __device__ static inline uint16_t from_f32(float v) { return f32_to_bf16_bits(v); }
+};
+
+// ---------------------------------------------------------------------------
+// OCP fp8 encoders (round to nearest even, saturate to the finite max, NaN ->
+// 0x7f). Derivation, e4m3fn (bias 7, max 1.75*2^8 = 448, min normal 2^-6,
+// subnormal step 2^-9):
+//   |x| >= 2^-6 : the fp32 exponent/mantissa fields shifted right by 20 keep 3
+//                 mantissa bits; adding 0x7ffff + lsb before the shift rounds
+//                 to nearest even, and subtracting (127-7)<<3 rebiases. A carry
+//                 out of the mantissa bumps the exponent, which is the correct
+//                 encoding of the rounded value.
+//   |x| <  2^-6 : the code equals rint(|x| * 2^9) (0..8); 8 is the encoding of
+//                 2^-6, so rounding up into the normal range is also right.
+// e5m2 is the same with bias 15, 2 mantissa bits, max 1.75*2^15 = 57344,
+// min normal 2^-14, subnormal step 2^-16.
+// ---------------------------------------------------------------------------
+__device__ inline uint8_t f32_to_e4m3(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return 0x7f;             // NaN
+  if (a > 0x43e00000u) return sign | 0x7eu;     // > 448 (incl. inf): saturate
+  uint32_t code;
+  if (a >= 0x3c800000u) {                       // >= 2^-6: normal
+    code = ((a + 0x7ffffu + ((a >> 20) & 1u)) >> 20) - (120u << 3);
+  } else {
+    code = static_cast<uint32_t>(__builtin_rintf(__uint_as_float(a) * 512.0f));
+  }
+  return static_cast<uint8_t>(sign | code);
+}
+
+__device__ inline uint8_t f32_to_e5m2(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return 0x7f;             // NaN
+  if (a > 0x47600000u) return sign | 0x7bu;     // > 57344 (incl. inf): saturate
+  uint32_t code;
+  if (a >= 0x38800000u) {                       // >= 2^-14: normal
+    code = ((a + 0xfffffu + ((a >> 21) & 1u)) >> 21) - (112u << 2);
+  } else {
+    code = static_cast<uint32_t>(__builtin_rintf(__uint_as_float(a) * 65536.0f));
+  }
+  return static_cast<uint8_t>(sign | code);
+}
+
+// Decoders (exact). e4m3fn: exponent field 15 with mantissa 7 is NaN.
+__device__ inline float e4m3_to_f32(uint8_t c) {
+  const uint32_t sign = static_cast<uint32_t>(c & 0x80u) << 24;
+  const uint32_t e = (c >> 3) & 0xfu, m = c & 7u;
+  if (e == 15u && m == 7u) return __uint_as_float(0x7fc00000u | sign);
+  float mag;
+  if (e == 0u) {
+    mag = static_cast<float>(m) * 0.001953125f;  // m * 2^-9
+  } else {
+    mag = __uint_as_float(((e + 120u) << 23) | (m << 20));
+  }
+  return __uint_as_float(__float_as_uint(mag) | sign);
+}
+
+__device__ inline float e5m2_to_f32(uint8_t c) {
+  const uint32_t sign = static_cast<uint32_t>(c & 0x80u) << 24;
+  const uint32_t e = (c >> 2) & 0x1fu, m = c & 3u;
+  if (e == 31u) return __uint_as_float((m ? 0x7fc00000u : 0x7f800000u) | sign);
+  float mag;
+  if (e == 0u) {
+    mag = static_cast<float>(m) * 1.52587890625e-05f;  // m * 2^-16
+  } else {
+    mag = __uint_as_float(((e + 112u) << 23) | (m << 21));
+  }
+  return __uint_as_float(__float_as_uint(mag) | sign);
+}
+
+struct e4m3_t {
+  static constexpr float qmax = 448.0f;
+  __device__ static inline uint8_t enc(float x) { return f32_to_e4m3(x); }
+  __device__ static inline float dec(uint8_t c) { return e4m3_to_f32(c); }
+};
+struct e5m2_t {
+  static constexpr float qmax = 57344.0f;
+  __device__ static inline uint8_t enc(float x) { return f32_to_e5m2(x); }
+  __device__ static inline float dec(uint8_t c) { return e5m2_to_f32(c); }
+};
+
+constexpr float kEpsScale = 1e-12f;  // floor of every dynamic scale
+constexpr float kInt8Max = 127.0f;
+
+// ---------------------------------------------------------------------------
+// wave64 reductions (xor butterflies over all 64 lanes)
+// ---------------------------------------------------------------------------
+__device__ inline float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Max over aligned groups of `width` lanes (width a power of two <= 64).
+__device__ inline float group_max(float v, int width) {
+  for (int o = width >> 1; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+}  // namespace ks

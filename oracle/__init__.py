@@ -1,0 +1,342 @@
+"""CPU oracle for the quantized-inference path -- TEST INFRASTRUCTURE ONLY.
+
+Restates the arithmetic of cklxx/kernel-set's reference kernels and of its
+benchmark references so the HIP library can be checked against it:
+
+* scalar C (``ks_oracle.c``, built by ``oracle/build.py``): fp8 codec,
+  quantizers, int4 repack/dequant, and scalar GEMMs in the reference kernels'
+  operation order;
+* NumPy: the "dequantize, then fp32 matmul" references of
+  ``benchmarks/bench.py:1228-1235,1274-1285,1434-1470`` that the GEMM
+  tolerances are stated against, plus small helpers (bf16 rounding, packing,
+  the reference tests' xorshift32 generator).
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline``
+leg may import this package, and only as the checker.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libks_oracle.so")
+
+E4M3, E5M2, INT8 = 0, 1, 2  # quantizer targets (fp8 formats share 0/1)
+QMAX = {E4M3: 448.0, E5M2: 57344.0, INT8: 127.0}
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load (building if needed) the scalar C oracle."""
+    global _lib
+    if _lib is None:
+        if not os.path.isfile(_LIB_PATH):
+            from . import build as _b
+            _b.build()
+        L = ctypes.CDLL(_LIB_PATH)
+        P = ctypes.c_void_p
+        I64 = ctypes.c_int64
+        I = ctypes.c_int
+        sig = {
+            "oracle_fp8_encode": [P, P, I64, I],
+            "oracle_fp8_decode": [P, P, I64, I],
+            "oracle_quant_group": [P, P, P, I64, I64, I64, I],
+            "oracle_quant_row": [P, P, P, I64, I64, I],
+            "oracle_quant_tensor": [P, P, P, I64, I],
+            "oracle_repack_int4": [P, P, P, I64, I64],
+            "oracle_dequant_int4": [P, P, P, P, I64, I64, I64],
+            "oracle_w4a16": [P, P, P, P, P, P, I64, I64, I64, I64],
+            "oracle_fp8_blockwise": [P, P, P, P, P, I64, I64, I64, I64, I64, I],
+            "oracle_w8a8_acc": [P, P, P, I64, I64, I64],
+            "oracle_w8a8_epilogue": [P, P, P, P, P, I64, I64, I, I],
+        }
+        for name, args in sig.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = None
+        _lib = L
+    return _lib
+
+
+def _p(arr):
+    return None if arr is None else arr.ctypes.data
+
+
+def _c(arr, dtype):
+    return np.ascontiguousarray(arr, dtype=dtype)
+
+
+# ---------------------------------------------------------------------------
+# 16-bit float helpers
+# ---------------------------------------------------------------------------
+def f32_to_bf16_bits(x) -> np.ndarray:
+    """fp32 -> bf16 bit patterns, round to nearest even (NaN -> quiet NaN)."""
+    u = _c(x, np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = np.isnan(_c(x, np.float32))
+    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+def bf16_bits_to_f32(h) -> np.ndarray:
+    return (_c(h, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def round_bf16(x) -> np.ndarray:
+    """Round fp32 values to the nearest bf16 value, returned as fp32."""
+    return bf16_bits_to_f32(f32_to_bf16_bits(x))
+
+
+def round_f16(x) -> np.ndarray:
+    return _c(x, np.float32).astype(np.float16).astype(np.float32)
+
+
+def round_to(x, dtype: str) -> np.ndarray:
+    if dtype == "bf16":
+        return round_bf16(x)
+    if dtype == "f16":
+        return round_f16(x)
+    return _c(x, np.float32)
+
+
+# ---------------------------------------------------------------------------
+# fp8 / int8 quantization (scalar C)
+# ---------------------------------------------------------------------------
+def fp8_encode(x, fmt: int = E4M3) -> np.ndarray:
+    x = _c(x, np.float32)
+    out = np.empty(x.shape, np.uint8)
+    lib().oracle_fp8_encode(_p(x), _p(out), x.size, fmt)
+    return out
+
+
+def fp8_decode(c, fmt: int = E4M3) -> np.ndarray:
+    c = _c(c, np.uint8)
+    out = np.empty(c.shape, np.float32)
+    lib().oracle_fp8_decode(_p(c), _p(out), c.size, fmt)
+    return out
+
+
+def quant_group(x, group_size: int, target: int = E4M3):
+    """Per-(row, 1 x group_size) dynamic quant (quant_fp8_group.cu:74-107).
+
+    Returns (codes uint8 [rows, cols], scale fp32 [rows, ceil(cols/gs)])."""
+    x = _c(x, np.float32)
+    rows, cols = x.shape
+    ng = (cols + group_size - 1) // group_size
+    out = np.empty((rows, cols), np.uint8)
+    sc = np.empty((rows, ng), np.float32)
+    lib().oracle_quant_group(_p(x), _p(out), _p(sc), rows, cols, group_size, target)
+    return out, sc
+
+
+def quant_row(x, target: int = E4M3):
+    """Per-token dynamic quant (quant_fp8.cu:42-66, quant_int8.cu:23-47)."""
+    x = _c(x, np.float32)
+    rows, cols = x.shape
+    out = np.empty((rows, cols), np.uint8)
+    sc = np.empty((rows,), np.float32)
+    lib().oracle_quant_row(_p(x), _p(out), _p(sc), rows, cols, target)
+    return out, sc
+
+
+def quant_tensor(x, target: int = E4M3):
+    """Per-tensor dynamic quant (quant_fp8.cu:69-100, quant_int8.cu:50-83)."""
+    x = _c(x, np.float32)
+    out = np.empty(x.shape, np.uint8)
+    sc = np.empty((1,), np.float32)
+    lib().oracle_quant_tensor(_p(x), _p(out), _p(sc), x.size, target)
+    return out, sc
+
+
+def dequant(codes, scale, target: int, per_token: bool) -> np.ndarray:
+    """float(code) * scale in fp32 (quant_fp8.cu:103-115, quant_int8.cu:86-99)."""
+    if target == INT8:
+        v = _c(codes, np.uint8).view(np.int8).astype(np.float32)
+    else:
+        v = fp8_decode(codes, target)
+    s = _c(scale, np.float32)
+    s = s.reshape(-1, 1) if per_token else s.reshape(1, 1)
+    return (v * s).astype(np.float32)
+
+
+# ---------------------------------------------------------------------------
+# int4 weight formats
+# ---------------------------------------------------------------------------
+def pack_k8_int32(codes) -> np.ndarray:
+    """codes uint8 [K, N] in 0..15 -> int32 [K/8, N], code k in nibble k % 8."""
+    q = _c(codes, np.uint32)
+    k, n = q.shape
+    q = q.reshape(k // 8, 8, n)
+    w = np.zeros((k // 8, n), np.uint32)
+    for j in range(8):
+        w |= q[:, j, :] << np.uint32(4 * j)
+    return w.view(np.int32)
+
+
+def pack_k2_uint8(codes) -> np.ndarray:
+    """codes [K, N] -> uint8 [K/2, N]: even k in bits 0-3, odd k in bits 4-7
+    (gemm_w4a16.cu:6-13)."""
+    q = _c(codes, np.uint8)
+    return (q[0::2] & 0xF) | ((q[1::2] & 0xF) << 4)
+
+
+def unpack_k2_uint8(b) -> np.ndarray:
+    b = _c(b, np.uint8)
+    kp, n = b.shape
+    out = np.empty((2 * kp, n), np.uint8)
+    out[0::2] = b & 0xF
+    out[1::2] = b >> 4
+    return out
+
+
+def repack_int4(qweight, perm=None) -> np.ndarray:
+    """repack_int4.cu:10-34 (+ act-order perm: output row k <- input row perm[k])."""
+    q = _c(qweight, np.int32).view(np.uint32)
+    k8, n = q.shape
+    out = np.empty((k8 * 4, n), np.uint8)
+    pp = None if perm is None else _c(perm, np.int32)
+    lib().oracle_repack_int4(_p(q), _p(pp), _p(out), k8 * 8, n)
+    return out
+
+
+def dequant_int4(qweight, scales, zeros, group_size: int) -> np.ndarray:
+    """dequant_int4.cu:47-58 in fp32 (caller rounds to the output dtype)."""
+    q = _c(qweight, np.int32).view(np.uint32)
+    k8, n = q.shape
+    s = _c(scales, np.float32)
+    z = _c(zeros, np.float32)
+    out = np.empty((k8 * 8, n), np.float32)
+    lib().oracle_dequant_int4(_p(q), _p(s), _p(z), _p(out), k8 * 8, n, group_size)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# GEMM references
+# ---------------------------------------------------------------------------
+def w4a16_scalar(a, b_packed, scales, zeros, group_size, bias=None) -> np.ndarray:
+    """gemm_w4a16.cu:74-129 order, fp32 result (before rounding to dtype)."""
+    a = _c(a, np.float32)
+    b = _c(b_packed, np.uint8)
+    m, k = a.shape
+    n = b.shape[1]
+    s = _c(scales, np.float32)
+    z = None if zeros is None else _c(zeros, np.float32)
+    bb = None if bias is None else _c(bias, np.float32)
+    out = np.empty((m, n), np.float32)
+    lib().oracle_w4a16(_p(a), _p(b), _p(s), _p(z), _p(bb), _p(out), m, n, k, group_size)
+    return out
+
+
+def w4a16_dequant_weight(b_packed, scales, zeros, group_size, dtype="bf16") -> np.ndarray:
+    """bench.py:1274-1284: codes -> (codes - z) * s in fp32, rounded to dtype."""
+    codes = unpack_k2_uint8(b_packed).astype(np.float32)
+    k = codes.shape[0]
+    g = np.arange(k) // group_size
+    z = 0.0 if zeros is None else _c(zeros, np.float32)[g]
+    w = (codes - z) * _c(scales, np.float32)[g]
+    return round_to(w, dtype)
+
+
+def w4a16_ref(a, b_packed, scales, zeros, group_size, dtype="bf16", bias=None,
+              weight=None) -> np.ndarray:
+    """bench.py:1274-1285: a.float() @ dequant(weight).float() (+ bias), fp32."""
+    if weight is None:
+        weight = w4a16_dequant_weight(b_packed, scales, zeros, group_size, dtype)
+    out = _c(a, np.float32) @ weight
+    if bias is not None:
+        out = out + _c(bias, np.float32)[None, :]
+    return out.astype(np.float32)
+
+
+def fp8_blockwise_scalar(a8, b8, a_scale, b_scale, block_n, block_k, fmt=E4M3):
+    """gemm_fp8_blockwise.cu:107-161 (two-level fp32 accumulation)."""
+    a8 = _c(a8, np.uint8)
+    b8 = _c(b8, np.uint8)
+    m, k = a8.shape
+    n = b8.shape[1]
+    out = np.empty((m, n), np.float32)
+    lib().oracle_fp8_blockwise(_p(a8), _p(b8), _p(_c(a_scale, np.float32)),
+                               _p(_c(b_scale, np.float32)), _p(out), m, n, k,
+                               block_n, block_k, fmt)
+    return out
+
+
+def fp8_blockwise_dequant(a8, b8, a_scale, b_scale, block_n, block_k, fmt=E4M3):
+    """bench.py:1460-1470: dequantize both operands with their block scales."""
+    a = fp8_decode(a8, fmt)
+    b = fp8_decode(b8, fmt)
+    m, k = a.shape
+    n = b.shape[1]
+    kb = np.arange(k) // block_k
+    nb = np.arange(n) // block_n
+    a_deq = a * _c(a_scale, np.float32)[:, kb]
+    b_deq = b * _c(b_scale, np.float32)[kb][:, nb]
+    return a_deq.astype(np.float32), b_deq.astype(np.float32)
+
+
+def fp8_blockwise_ref(a8, b8, a_scale, b_scale, block_n=128, block_k=128, fmt=E4M3):
+    """bench.py:1502: a_deq @ b_deq in fp32."""
+    a_deq, b_deq = fp8_blockwise_dequant(a8, b8, a_scale, b_scale, block_n, block_k, fmt)
+    return (a_deq @ b_deq).astype(np.float32)
+
+
+def w8a8_acc(a_i8, b_i8) -> np.ndarray:
+    """Exact int32 accumulators A @ B (bench.py:1228 does it in fp64: every
+    |partial sum| < 2^53, so fp64 BLAS is exact)."""
+    a = _c(a_i8, np.int8).astype(np.float64)
+    b = _c(b_i8, np.int8).astype(np.float64)
+    acc = a @ b
+    return acc.astype(np.int64).astype(np.int32)
+
+
+def w8a8_acc_scalar(a_i8, b_i8) -> np.ndarray:
+    a = _c(a_i8, np.int8)
+    b = _c(b_i8, np.int8)
+    m, k = a.shape
+    n = b.shape[1]
+    out = np.empty((m, n), np.int32)
+    lib().oracle_w8a8_acc(_p(a), _p(b), _p(out), m, n, k)
+    return out
+
+
+def w8a8_epilogue(acc, a_scale, b_scale, bias=None, a_per_token=True,
+                  b_per_channel=True) -> np.ndarray:
+    """gemm_w8a8.cu:134-141: (float(acc) * a_s) * b_s (+ bias), fp32."""
+    acc = _c(acc, np.int32)
+    m, n = acc.shape
+    out = np.empty((m, n), np.float32)
+    bb = None if bias is None else _c(bias, np.float32)
+    lib().oracle_w8a8_epilogue(_p(acc), _p(_c(a_scale, np.float32)),
+                               _p(_c(b_scale, np.float32)), _p(bb), _p(out), m, n,
+                               int(a_per_token), int(b_per_channel))
+    return out
+
+
+# ---------------------------------------------------------------------------
+# misc
+# ---------------------------------------------------------------------------
+def xorshift32_uniform(n: int, seed: int, lo: float = -2.0, hi: float = 2.0) -> np.ndarray:
+    """The reference tests' deterministic generator (test_common.cuh:205-220),
+    computed in fp32 like the C++ it restates."""
+    s = seed if seed else 0x9E3779B9
+    out = np.empty(n, np.float32)
+    lo32, span = np.float32(lo), np.float32(hi) - np.float32(lo)
+    for i in range(n):
+        s ^= (s << 13) & 0xFFFFFFFF
+        s ^= s >> 17
+        s ^= (s << 5) & 0xFFFFFFFF
+        u = np.float32(s) / np.float32(4294967295.0)
+        out[i] = lo32 + u * span
+    return out
+
+
+def rel_err(out, ref) -> float:
+    """max |out - ref| / max |ref| (bench.py:847-852), in fp64."""
+    o = np.asarray(out, np.float64)
+    r = np.asarray(ref, np.float64)
+    denom = max(float(np.abs(r).max()) if r.size else 0.0, 1e-6)
+    return float(np.abs(o - r).max()) / denom if r.size else 0.0

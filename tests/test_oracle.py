@@ -1,0 +1,261 @@
+"""Pins for the CPU oracle itself (no GPU).
+
+Each check is chosen so a plausible oracle mistake (wrong rounding direction,
+dropped zero-point, transposed operand, division instead of reciprocal-multiply)
+fails it: torch's independent fp8 casts, exact midpoints, closed forms,
+brute-force loops, integer special cases, and the reference's own
+test_quant.cu case with its +-1 acceptance criterion.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+# ---------------------------------------------------------------- fp8 codec
+@pytest.mark.parametrize("fmt,tdt", [(O.E4M3, torch.float8_e4m3fn), (O.E5M2, torch.float8_e5m2)])
+def test_fp8_decode_matches_torch_all_codes(fmt, tdt):
+    c = np.arange(256, dtype=np.uint8)
+    ours = O.fp8_decode(c, fmt)
+    theirs = torch.from_numpy(c).view(tdt).float().numpy()
+    assert np.array_equal(np.isnan(ours), np.isnan(theirs))
+    fin = ~np.isnan(ours)
+    assert np.array_equal(ours[fin], theirs[fin])
+
+
+@pytest.mark.parametrize("fmt", [O.E4M3, O.E5M2])
+def test_fp8_roundtrip_every_finite_code(fmt):
+    c = np.arange(256, dtype=np.uint8)
+    d = O.fp8_decode(c, fmt)
+    fin = np.isfinite(d)
+    assert np.array_equal(O.fp8_encode(d[fin], fmt), c[fin])
+
+
+@pytest.mark.parametrize("fmt,tdt", [(O.E4M3, torch.float8_e4m3fn), (O.E5M2, torch.float8_e5m2)])
+def test_fp8_midpoints_round_half_even(fmt, tdt):
+    # Exact midpoints between consecutive positive finite values: RNE picks the
+    # code with an even mantissa LSB. Checked against the rule and torch.
+    c = np.arange(0, 0x7F, dtype=np.uint8)
+    d = O.fp8_decode(c, fmt).astype(np.float64)
+    fin = np.isfinite(d)
+    c, d = c[fin], d[fin]
+    mids = ((d[:-1] + d[1:]) / 2).astype(np.float32)
+    assert np.array_equal(mids.astype(np.float64), (d[:-1] + d[1:]) / 2)  # exact in fp32
+    enc = O.fp8_encode(mids, fmt)
+    even = np.where(c[:-1] % 2 == 0, c[:-1], c[1:])
+    assert np.array_equal(enc, even)
+    assert np.array_equal(enc, torch.from_numpy(mids).to(tdt).view(torch.uint8).numpy())
+    # and just either side of each midpoint rounds to the nearer code
+    lo = np.nextafter(mids, np.float32(0))
+    hi = np.nextafter(mids, np.float32(np.inf))
+    assert np.array_equal(O.fp8_encode(lo, fmt), c[:-1])
+    assert np.array_equal(O.fp8_encode(hi, fmt), c[1:])
+
+
+@pytest.mark.parametrize("fmt,tdt,fmax", [(O.E4M3, torch.float8_e4m3fn, 448.0),
+                                          (O.E5M2, torch.float8_e5m2, 57344.0)])
+def test_fp8_random_in_range_matches_torch(fmt, tdt, fmax):
+    rng = np.random.default_rng(1)
+    x = np.concatenate([
+        rng.standard_normal(200_000) * fmax / 3,
+        rng.standard_normal(50_000) * 1e-2,
+        rng.standard_normal(50_000) * 1e-5,
+    ]).astype(np.float32)
+    x = np.clip(x, -fmax, fmax)
+    ours = O.fp8_encode(x, fmt)
+    theirs = torch.from_numpy(x).to(tdt).view(torch.uint8).numpy()
+    assert np.array_equal(ours, theirs)
+
+
+def test_fp8_saturation_and_nan():
+    big = np.array([448.5, 463.9, 464.0, 1e6, np.inf], np.float32)
+    assert np.array_equal(O.fp8_encode(big, O.E4M3), np.full(5, 0x7E, np.uint8))
+    assert np.array_equal(O.fp8_encode(-big, O.E4M3), np.full(5, 0xFE, np.uint8))
+    big5 = np.array([57345.0, 61439.0, 61440.0, 1e9, np.inf], np.float32)
+    assert np.array_equal(O.fp8_encode(big5, O.E5M2), np.full(5, 0x7B, np.uint8))
+    assert O.fp8_encode(np.array([np.nan], np.float32), O.E4M3)[0] == 0x7F
+    assert O.fp8_encode(np.array([-0.0], np.float32), O.E4M3)[0] == 0x80
+
+
+# ------------------------------------------------------------- quantizers
+def _np_scale(amax, qmax):
+    return np.maximum(np.float32(amax) / np.float32(qmax), np.float32(1e-12)).astype(np.float32)
+
+
+def test_int8_ties_and_extremes():
+    # amax = 127 -> scale exactly 1, inv exactly 1: codes are rint(x), half-even
+    x = np.array([[127.0, 0.5, 1.5, 2.5, -0.5, -1.5, -127.0, 126.5]], np.float32)
+    q, s = O.quant_row(x, O.INT8)
+    assert s[0] == np.float32(1.0)
+    assert q.view(np.int8).tolist() == [[127, 0, 2, 2, 0, -2, -127, 126]]
+
+
+def test_all_zero_row_scale_floor():
+    q, s = O.quant_row(np.zeros((2, 10), np.float32), O.INT8)
+    assert np.all(s == np.float32(1e-12)) and np.all(q == 0)
+    q, s = O.quant_group(np.zeros((1, 300), np.float32), 128, O.E4M3)
+    assert np.all(s == np.float32(1e-12)) and np.all(q == 0)
+
+
+def test_amax_maps_to_qmax():
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((16, 256)).astype(np.float32)
+    q, s = O.quant_row(x, O.E4M3)
+    arg = np.abs(x).argmax(axis=1)
+    codes = q[np.arange(16), arg]
+    assert np.all((codes & 0x7F) == 0x7E)  # +-448
+    q8, _ = O.quant_row(x, O.INT8)
+    assert np.all(np.abs(q8.view(np.int8)[np.arange(16), arg].astype(int)) == 127)
+
+
+def test_reference_int8_case_xorshift():
+    # kernels/tests/test_quant.cu:34-139 on the same generated inputs: scales
+    # match max(amax/127, eps) and codes are within +-1 of rint(x / scale)
+    # (the reference's own acceptance), and exactly equal to the reciprocal-
+    # multiply form the reference kernel uses (quant_int8.cu:44).
+    x = O.xorshift32_uniform(6 * 130, 11, -5.0, 5.0).reshape(6, 130)
+    for dt in ("f32", "f16", "bf16"):
+        xs = O.round_to(x, dt)
+        q, s = O.quant_row(xs, O.INT8)
+        exp_s = _np_scale(np.abs(xs).max(axis=1), 127.0)
+        assert np.array_equal(s, exp_s)
+        div = np.clip(np.rint(xs / exp_s[:, None]), -127, 127)
+        assert np.abs(q.view(np.int8) - div).max() <= 1
+        inv = (np.float32(1.0) / exp_s).astype(np.float32)
+        mul = np.rint(np.clip((xs * inv[:, None]).astype(np.float32), -127, 127))
+        assert np.array_equal(q.view(np.int8).astype(np.float32), mul)
+        qt, st = O.quant_tensor(xs, O.INT8)
+        assert st[0] == _np_scale(np.abs(xs).max(), 127.0)
+
+
+def test_fp8_group_closed_form_numpy():
+    rng = np.random.default_rng(4)
+    x = O.round_bf16(rng.standard_normal((5, 200)).astype(np.float32) * 3)
+    q, s = O.quant_group(x, 64, O.E4M3)
+    for g in range(4):
+        blk = x[:, g * 64:(g + 1) * 64]
+        sc = _np_scale(np.abs(blk).max(axis=1), 448.0)
+        assert np.array_equal(s[:, g], sc)
+        inv = (np.float32(1.0) / sc).astype(np.float32)
+        expect = torch.from_numpy((blk * inv[:, None]).astype(np.float32)).to(
+            torch.float8_e4m3fn).view(torch.uint8).numpy()
+        assert np.array_equal(q[:, g * 64:(g + 1) * 64], expect)
+
+
+def test_golden_fixtures_regenerate_identically():
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("mg", os.path.join(GOLDEN, "make_golden.py"))
+    mg = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mg)
+    for name, fn in mg.FIXTURES.items():
+        fresh = fn()
+        saved = np.load(os.path.join(GOLDEN, name + ".npz"))
+        assert set(saved.files) == set(fresh)
+        for key in saved.files:
+            assert np.array_equal(saved[key], fresh[key]), (name, key)
+
+
+# ----------------------------------------------------------- int4 formats
+def test_repack_brute_force():
+    rng = np.random.default_rng(6)
+    k, n = 24, 5
+    codes = rng.integers(0, 16, (k, n), dtype=np.uint8)
+    words = O.pack_k8_int32(codes)
+    for kk in range(k):  # the int32 layout: nibble kk % 8 of word kk // 8
+        for c in range(n):
+            assert (int(words.view(np.uint32)[kk // 8, c]) >> (4 * (kk % 8))) & 0xF == codes[kk, c]
+    out = O.repack_int4(words)
+    for kp in range(k // 2):
+        for c in range(n):
+            assert out[kp, c] == (codes[2 * kp, c] | (codes[2 * kp + 1, c] << 4))
+    assert np.array_equal(O.unpack_k2_uint8(out), codes)
+    perm = rng.permutation(k).astype(np.int32)
+    assert np.array_equal(O.unpack_k2_uint8(O.repack_int4(words, perm)), codes[perm])
+
+
+def test_dequant_int4_closed_form():
+    rng = np.random.default_rng(8)
+    k, n, gs = 32, 6, 16
+    codes = rng.integers(0, 16, (k, n), dtype=np.uint8)
+    s = rng.uniform(0.01, 0.1, (k // gs, n)).astype(np.float32)
+    z = rng.integers(6, 10, (k // gs, n)).astype(np.float32)
+    out = O.dequant_int4(O.pack_k8_int32(codes), s, z, gs)
+    g = np.arange(k) // gs
+    assert np.array_equal(out, ((codes.astype(np.float32) - z[g]) * s[g]).astype(np.float32))
+
+
+# ------------------------------------------------------------------ GEMMs
+def test_w4a16_integer_special_case_exact():
+    # z = 8, s = 1 and small integer activations: the product is an exact
+    # integer matmul of (q - 8); the oracle must reproduce it exactly.
+    rng = np.random.default_rng(10)
+    m, k, n, gs = 4, 128, 24, 32
+    a = rng.integers(-3, 4, (m, k)).astype(np.float32)
+    codes = rng.integers(0, 16, (k, n), dtype=np.uint8)
+    s = np.ones((k // gs, n), np.float32)
+    z = np.full((k // gs, n), 8.0, np.float32)
+    exact = a.astype(np.int64) @ (codes.astype(np.int64) - 8)
+    b = O.pack_k2_uint8(codes)
+    assert np.array_equal(O.w4a16_scalar(a, b, s, z, gs), exact.astype(np.float32))
+    assert np.array_equal(O.w4a16_ref(a, b, s, z, gs), exact.astype(np.float32))
+    # zeros = None means zero-point 0
+    assert np.array_equal(O.w4a16_scalar(a, b, s, None, gs),
+                          (a.astype(np.int64) @ codes.astype(np.int64)).astype(np.float32))
+
+
+def test_w4a16_scalar_vs_bench_reference():
+    f = np.load(os.path.join(GOLDEN, "w4a16_small.npz"))
+    ref = O.w4a16_ref(f["a"], f["b_packed"], f["scales"], f["zeros"], int(f["gs"]),
+                      bias=f["bias"])
+    assert O.rel_err(f["c_f32"], ref) < 1e-2
+    # a zero-point error of one code unit would move the result far more
+    ref_bad = O.w4a16_ref(f["a"], f["b_packed"], f["scales"], f["zeros"] + 1, int(f["gs"]),
+                          bias=f["bias"])
+    assert O.rel_err(f["c_f32"], ref_bad) > 5e-2
+
+
+def test_fp8_blockwise_integer_special_case_exact():
+    rng = np.random.default_rng(12)
+    m, n, k = 9, 20, 70
+    a_int = rng.integers(-8, 9, (m, k)).astype(np.float32)  # exactly representable
+    b_int = rng.integers(-8, 9, (k, n)).astype(np.float32)
+    a8, b8 = O.fp8_encode(a_int), O.fp8_encode(b_int)
+    ones_a = np.ones((m, -(-k // 32)), np.float32)
+    ones_b = np.ones((-(-k // 32), -(-n // 16)), np.float32)
+    exact = (a_int.astype(np.int64) @ b_int.astype(np.int64)).astype(np.float32)
+    assert np.array_equal(O.fp8_blockwise_scalar(a8, b8, ones_a, ones_b, 16, 32), exact)
+    assert np.array_equal(O.fp8_blockwise_ref(a8, b8, ones_a, ones_b, 16, 32), exact)
+
+
+def test_fp8_blockwise_scalar_vs_dequant_reference():
+    f = np.load(os.path.join(GOLDEN, "fp8_blockwise_small.npz"))
+    bn, bk = int(f["bn"]), int(f["bk"])
+    ref = O.fp8_blockwise_ref(f["a8"], f["b8"], f["a_scale"], f["b_scale"], bn, bk)
+    assert O.rel_err(f["c_f32"], ref) < 1e-5
+    # transposing the weight-scale grid must be caught
+    bad = O.fp8_blockwise_ref(f["a8"], f["b8"], f["a_scale"], f["b_scale"][:, ::-1].copy(), bn, bk)
+    assert O.rel_err(f["c_f32"], bad) > 1e-2
+
+
+def test_w8a8_accumulators_three_ways():
+    rng = np.random.default_rng(14)
+    a = rng.integers(-127, 128, (7, 50)).astype(np.int8)
+    b = rng.integers(-127, 128, (50, 9)).astype(np.int8)
+    brute = [[sum(int(a[i, t]) * int(b[t, j]) for t in range(50)) for j in range(9)]
+             for i in range(7)]
+    assert O.w8a8_acc_scalar(a, b).tolist() == brute
+    assert O.w8a8_acc(a, b).tolist() == brute
+
+
+def test_w8a8_epilogue_order():
+    acc = np.array([[3, -5]], np.int32)
+    a_s = np.array([0.1], np.float32)
+    b_s = np.array([0.3, 0.7], np.float32)
+    out = O.w8a8_epilogue(acc, a_s, b_s)
+    exp = ((acc.astype(np.float32) * a_s[0]).astype(np.float32) * b_s).astype(np.float32)
+    assert np.array_equal(out, exp)
