@@ -1,16 +1,20 @@
 """Benchmark: kernel-set quantized-inference path on one MI355X.
 
 Headline (``value``): W4A16 GEMV achieved HBM GB/s at M=1, K=N=4096, g=128
-(BASELINE config 1 shape, the north_star's >=70%-of-HBM target), with the
-weights cold: ``--rotate`` distinct weight sets (default 64 x 8.9 MB = 571 MB,
-over twice the 256 MB MALL) are cycled so every call streams from HBM.
-A step is one ks_gemm_w4a16 call. Secondary lines (same JSON object) cover the
-fp8 blockwise GEMM (config 3), the per-token-group fp8 quantizer, the W4A16
-sweep (config 2), W8A8 (config 4) and the MoE grouped W4A16 (config 5).
+(BASELINE config 1 shape, the north_star's >=70%-of-HBM target), weights cold:
+``--rotate`` distinct weight sets (default 64 x 8.9 MB = 571 MB, over twice the
+256 MB MALL) are cycled so every call streams its weights from HBM. A step is
+one ks_gemm_w4a16 call.
 
-Timing: HIP events recorded on the stream the kernels run on (torch's current
-stream, which the library launches on) around exactly --steps calls after
---warmup untimed calls; time per call = elapsed / steps.
+Secondary lines (key ``secondary``) cover every BASELINE config: the fp8
+blockwise GEMM and its 1x128 activation quantizer (config 3, the second half of
+the metric), the W4A16 sweep (config 2), W8A8 (config 4) and the MoE grouped
+W4A16 GEMM (config 5).
+
+Timing: calls are captured into a HIP graph (so host launch overhead is not
+measured) and replayed; HIP events recorded on the replay stream bracket
+exactly the timed calls, after untimed warm-up replays. Time per call =
+elapsed / calls.
 
 cpu_baseline: the oracle's restatement of the reference's torch CPU path
 (dequantize, then fp32 matmul; bench.py:1274-1285 of the reference) on the
@@ -32,10 +36,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "kernel-set_amd"))
 sys.path.insert(0, ROOT)
 
-HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
-FP8_PEAK_TFLOPS = 5000.0     # dense fp8 MFMA
-BF16_PEAK_TFLOPS = 2500.0    # dense bf16 MFMA
-INT8_PEAK_TOPS = 5000.0      # dense int8 MFMA
+HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
+PEAK_TFLOPS = {"fp8": 5000.0, "bf16": 2500.0, "int8": 5000.0}  # dense MFMA
 METRIC = "W4A16 GEMV HBM GB/s (% peak) @M=1; fp8-block GEMM TFLOP/s (% peak) @M=2048"
 
 
@@ -43,45 +45,138 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def time_calls(torch, fn, steps, warmup, rotate=1):
-    """Average device time per call over exactly `steps` calls (events on the
-    current stream), after `warmup` untimed calls. fn(i) runs call i."""
-    for i in range(warmup):
-        fn(i % rotate)
-    torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record()
-    for i in range(steps):
-        fn(i % rotate)
-    end.record()
-    torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps  # ms per call
+class Timer:
+    """Graph-captured replay timing on a dedicated stream."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.stream = torch.cuda.Stream()
+
+    def run(self, fn, per_graph, steps, warmup):
+        """fn(i) issues call i (i < per_graph). Returns (ms per call, calls timed)."""
+        torch = self.torch
+        with torch.cuda.stream(self.stream):
+            for i in range(per_graph):  # eager warm-up: allocates library scratch
+                fn(i)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=self.stream):
+            for i in range(per_graph):
+                fn(i)
+        replays = max(1, -(-steps // per_graph))
+        with torch.cuda.stream(self.stream):
+            for _ in range(max(1, -(-warmup // per_graph))):
+                g.replay()
+            torch.cuda.synchronize()
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            start.record()
+            for _ in range(replays):
+                g.replay()
+            end.record()
+        torch.cuda.synchronize()
+        calls = replays * per_graph
+        ms = start.elapsed_time(end) / calls
+        del g
+        return ms, calls
+
+
+def rot_copies(t, n):
+    return [t] + [t.clone() for _ in range(n - 1)]
 
 
 # ---------------------------------------------------------------------------
-# workloads
+# workloads: each returns (fn, per_graph, bytes/call, flops/call, extra)
 # ---------------------------------------------------------------------------
-def w4a16_workload(torch, ks, H, m, k, n, gs, zero_mode, rotate, seed=0):
-    a, codes, s, z = H.w4a16_inputs(m, k, n, gs, zero_mode, seed)
+def wl_w4a16(torch, ks, H, m, k, n, gs, zero_mode, rotate, seed=0):
     import oracle as O
-    b0 = O.pack_k2_uint8(codes)
+    a, codes, s, z = H.w4a16_inputs(m, k, n, gs, zero_mode, seed)
     at, _ = H.to_dev(a, "bf16")
-    st, _ = H.to_dev(s, "bf16")
-    zt, _ = H.to_dev(z, "bf16")
-    bt = H.np_u8_dev(b0)
-    # rotated copies: distinct buffers with the same contents (cold weights)
-    bs = [bt] + [bt.clone() for _ in range(rotate - 1)]
-    ss = [st] + [st.clone() for _ in range(rotate - 1)]
-    zs = [zt] + [zt.clone() for _ in range(rotate - 1)]
+    bs = rot_copies(H.np_u8_dev(O.pack_k2_uint8(codes)), rotate)
+    ss = rot_copies(H.to_dev(s, "bf16")[0], rotate)
+    zs = rot_copies(H.to_dev(z, "bf16")[0], rotate)
     c = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
 
     def fn(i):
         ks.gemm.gemm_w4a16(c, at, bs[i], ss[i], zs[i], m, n, k, gs)
 
     nbytes = (k // 2) * n + 2 * (k // gs) * n * 2 + m * k * 2 + m * n * 2
-    flops = 2.0 * m * n * k
-    return fn, nbytes, flops
+    return fn, rotate, nbytes, 2.0 * m * n * k
+
+
+def wl_quant_group(torch, ks, H, rotate):
+    rows, cols = 2048, 7168
+    rng = np.random.default_rng(33)
+    x = rng.standard_normal((rows, cols)).astype(np.float32)
+    xs = rot_copies(H.to_dev(x, "bf16")[0], rotate)
+    out = torch.empty(rows, cols, device="cuda", dtype=torch.float8_e4m3fn)
+    sc = torch.empty(rows, cols // 128, device="cuda", dtype=torch.float32)
+
+    def fn(i):
+        ks.quant.quantize_fp8_group(out, sc, xs[i], rows, cols, group_size=128)
+
+    nbytes = rows * cols * 2 + rows * cols + rows * (cols // 128) * 4
+    return fn, rotate, nbytes, 0.0
+
+
+def wl_fp8_gemm(torch, ks, H):
+    import oracle as O
+    m, n, k = 2048, 7168, 7168
+    rng = np.random.default_rng(7)
+    a8 = torch.from_numpy(O.fp8_encode(rng.standard_normal((m, k)).astype(np.float32) * 50)).cuda()
+    b8 = torch.from_numpy(O.fp8_encode(rng.standard_normal((k, n)).astype(np.float32) * 50)).cuda()
+    a_s = torch.from_numpy(rng.uniform(0.001, 0.01, (m, k // 128)).astype(np.float32)).cuda()
+    b_s = torch.from_numpy(rng.uniform(0.001, 0.01, (k // 128, n // 128)).astype(np.float32)).cuda()
+    a8 = a8.view(torch.float8_e4m3fn)
+    b8 = b8.view(torch.float8_e4m3fn)
+    out = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+
+    def fn(i):
+        ks.gemm.gemm_fp8_blockwise(out, a8, b8, a_s, b_s, m, n, k)
+
+    nbytes = m * k + k * n + m * n * 2 + a_s.numel() * 4 + b_s.numel() * 4
+    return fn, 8, nbytes, 2.0 * m * n * k
+
+
+def wl_w8a8(torch, ks, H):
+    m = n = k = 4096
+    rng = np.random.default_rng(8)
+    a = torch.from_numpy(rng.integers(-127, 128, (m, k)).astype(np.int8)).cuda()
+    b = torch.from_numpy(rng.integers(-127, 128, (k, n)).astype(np.int8)).cuda()
+    a_s = torch.rand(m, device="cuda") * 0.02 + 0.01
+    b_s = torch.rand(n, device="cuda") * 0.02 + 0.01
+    out = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+
+    def fn(i):
+        ks.gemm.gemm_w8a8(out, a, b, a_s, b_s, m, n, k)
+
+    return fn, 8, m * k + k * n + m * n * 2, 2.0 * m * n * k
+
+
+def wl_moe(torch, ks, H, K, N, rotate):
+    import oracle as O
+    E, T, top_k, gs = 64, 256, 8, 128
+    rng = np.random.default_rng(K)
+    ids = O.moe_topk_ids(rng.standard_normal((T, E)).astype(np.float32), top_k)
+    row_src, offs = O.moe_group_rows(ids, E, 16)
+    a = np.zeros((len(row_src), K), np.float32)
+    live = row_src >= 0
+    a[live] = rng.standard_normal((int(live.sum()), K)).astype(np.float32)
+    at, _ = H.to_dev(a, "bf16")
+    b = np.stack([O.pack_k2_uint8(rng.integers(0, 16, (K, N), dtype=np.uint8)) for _ in range(E)])
+    bs = rot_copies(H.np_u8_dev(b), rotate)
+    s = rng.uniform(0.002, 0.02, (E, K // gs, N)).astype(np.float32)
+    ss = rot_copies(H.to_dev(s, "bf16")[0], rotate)
+    zs = rot_copies(H.to_dev(np.full_like(s, 8.0), "bf16")[0], rotate)
+    offt = H.np_i32_dev(offs)
+    c = torch.empty(len(row_src), N, device="cuda", dtype=torch.bfloat16)
+    rows = int(live.sum())
+
+    def fn(i):
+        ks.moe.grouped_gemm_w4a16(c, at, bs[i], ss[i], zs[i], offt, E, len(row_src), N, K, gs)
+
+    nbytes = E * (K // 2) * N + 2 * E * (K // gs) * N * 2 + rows * K * 2 + rows * N * 2
+    return fn, rotate, nbytes, 2.0 * rows * N * K
 
 
 def cpu_baseline_w4a16(H, m, k, n, gs, budget_s=10.0):
@@ -91,31 +186,43 @@ def cpu_baseline_w4a16(H, m, k, n, gs, budget_s=10.0):
     b = O.pack_k2_uint8(codes)
     av, sv, zv = O.round_bf16(a), O.round_bf16(s), O.round_bf16(z)
     O.w4a16_ref(av, b, sv, zv, gs, "bf16")  # warm-up
-    reps, t0 = 0, time.perf_counter()
     times = []
-    while time.perf_counter() - t0 < budget_s or reps < 3:
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < budget_s or len(times) < 3:
         t1 = time.perf_counter()
         O.w4a16_ref(av, b, sv, zv, gs, "bf16")
         times.append(time.perf_counter() - t1)
-        reps += 1
     med = float(np.median(times))
     nbytes = (k // 2) * n + 2 * (k // gs) * n * 2 + m * k * 2 + m * n * 2
     return {
-        "value": nbytes / med / 1e9, "unit": "GB/s",
+        "value": round(nbytes / med / 1e9, 4), "unit": "GB/s",
         "cores": int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)),
         "kind": "port",
-        "sample": (f"{reps} repetitions of W4A16 M={m} K={k} N={n} g={gs}: oracle "
+        "sample": (f"{len(times)} repetitions of W4A16 M={m} K={k} N={n} g={gs}: oracle "
                    f"unpack + (q-z)*s -> bf16 + fp32 matmul (numpy BLAS), median "
                    f"{med * 1e3:.2f} ms per call"),
-        "ms_per_call": med * 1e3,
     }
+
+
+def line(name, ms, calls, nbytes, flops, bound, peak_key=None):
+    d = {"us_per_call": round(ms * 1e3, 3), "calls": calls, "bytes": nbytes,
+         "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 2)}
+    if flops:
+        d["TFLOP/s"] = round(flops / (ms * 1e-3) / 1e12, 2)
+    if bound == "hbm":
+        d["roofline_frac"] = round(d["GB/s"] / HBM_PEAK_GBS, 4)
+    else:
+        d["roofline_frac"] = round(d["TFLOP/s"] / PEAK_TFLOPS[peak_key], 4)
+    d["bound"] = bound if bound == "hbm" else f"mfma-{peak_key}"
+    log(f"{name}: {d}")
+    return d
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000)
-    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--steps", type=int, default=1024)
+    ap.add_argument("--warmup", type=int, default=128)
     ap.add_argument("--rotate", type=int, default=64)
     ap.add_argument("--only", default="all", help="all | headline")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
@@ -123,33 +230,34 @@ def main():
 
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only: kernel-set is a "
-                                   "single-device kernel library and every GPU box "
-                                   "here has one GPU; run with --gpus 1"}))
+                                   "single-device kernel library and every GPU box here "
+                                   "has one GPU; run with --gpus 1"}))
         sys.exit(2)
 
     import torch
     import kernel_set as ks
     from tests import helpers as H
 
-    torch.manual_seed(0)
     dev_name = torch.cuda.get_device_name(0)
-    log(f"device: {dev_name}")
+    props = torch.cuda.get_device_properties(0)
+    log(f"device: {dev_name} {getattr(props, 'gcnArchName', '')} CUs={props.multi_processor_count}")
+    T = Timer(torch)
 
     # ---- headline: W4A16 GEMV, config 1 shape, cold weights ----------------
     m, k, n, gs = 1, 4096, 4096, 128
-    fn, nbytes, flops = w4a16_workload(torch, ks, H, m, k, n, gs, "fixed8", args.rotate)
-    ms = time_calls(torch, fn, args.steps, args.warmup, args.rotate)
+    fn, per, nbytes, flops = wl_w4a16(torch, ks, H, m, k, n, gs, "fixed8", args.rotate)
+    ms, calls = T.run(fn, per, args.steps, args.warmup)
     gbs = nbytes / (ms * 1e-3) / 1e9
-    log(f"w4a16 gemv M=1 K=N=4096: {ms * 1e3:.2f} us/call, {gbs:.1f} GB/s")
-    warm_fn, _, _ = w4a16_workload(torch, ks, H, m, k, n, gs, "fixed8", 1)
-    ms_warm = time_calls(torch, warm_fn, args.steps, args.warmup, 1)
+    log(f"w4a16 gemv M=1 K=N=4096 (cold): {ms * 1e3:.3f} us/call, {gbs:.1f} GB/s")
+    wfn, wper, _, _ = wl_w4a16(torch, ks, H, m, k, n, gs, "fixed8", 1)
+    ms_warm, _ = T.run(wfn, wper, args.steps, args.warmup)
 
     result = {
         "metric": METRIC,
         "value": round(gbs, 2),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": calls,
         "warmup": args.warmup,
         "ms_per_step": ms,
         "higher_is_better": True,
@@ -159,13 +267,44 @@ def main():
         "data": "synthetic (BASELINE config 1 distributions, seeded)",
         "config": {"workload": "w4a16_gemv", "M": m, "K": k, "N": n, "group_size": gs,
                    "zeros": "fixed 8.0", "weights": f"cold: {args.rotate} rotated copies",
+                   "timing": "HIP-graph replay, events on the replay stream",
                    "device": dev_name},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "gemv_kernel", "bytes_per_launch": nbytes},
+                     "kernel": "ks::w4a16::gemv_kernel", "bytes_per_launch": nbytes},
         "warm_cache": {"us_per_call": round(ms_warm * 1e3, 3),
                        "GB/s": round(nbytes / (ms_warm * 1e-3) / 1e9, 2)},
     }
+
+    if args.only != "headline":
+        sec = {}
+        steps = max(64, args.steps // 8)
+        fn, per, nb, fl = wl_fp8_gemm(torch, ks, H)
+        ms2, c2 = T.run(fn, per, max(32, steps // 8), 8)
+        sec["fp8_blockwise_gemm_M2048_N7168_K7168"] = line("fp8 gemm", ms2, c2, nb, fl, "mfma", "fp8")
+        fn, per, nb, fl = wl_quant_group(torch, ks, H, 16)
+        ms2, c2 = T.run(fn, per, steps, 32)
+        sec["quant_fp8_group_2048x7168_cold"] = line("quant group", ms2, c2, nb, fl, "hbm")
+        for mm in (1, 16, 64, 256):
+            fn, per, nb, fl = wl_w4a16(torch, ks, H, mm, 4096, 14336, 128, "int69", 16, seed=mm)
+            ms2, c2 = T.run(fn, per, steps, 32)
+            t_roof = max(nb / (HBM_PEAK_GBS * 1e9), fl / (PEAK_TFLOPS["bf16"] * 1e12))
+            d = line(f"w4a16 M={mm}", ms2, c2, nb, fl, "hbm")
+            d["roofline_frac"] = round(t_roof / (ms2 * 1e-3), 4)
+            d["bound"] = "hbm" if nb / (HBM_PEAK_GBS * 1e9) >= fl / (PEAK_TFLOPS["bf16"] * 1e12) else "mfma-bf16"
+            sec[f"w4a16_M{mm}_K4096_N14336_cold"] = d
+        fn, per, nb, fl = wl_w8a8(torch, ks, H)
+        ms2, c2 = T.run(fn, per, max(32, steps // 8), 8)
+        sec["w8a8_M4096_N4096_K4096"] = line("w8a8", ms2, c2, nb, fl, "mfma", "int8")
+        for K_, N_, nm in ((2048, 1536, "gate_up"), (768, 2048, "down")):
+            fn, per, nb, fl = wl_moe(torch, ks, H, K_, N_, 4)
+            ms2, c2 = T.run(fn, per, steps, 16)
+            sec[f"moe_w4a16_{nm}_E64_top8_T256_cold"] = line(f"moe {nm}", ms2, c2, nb, fl, "hbm")
+        result["secondary"] = sec
+        fp8 = sec["fp8_blockwise_gemm_M2048_N7168_K7168"]
+        result["fp8_gemm_tflops"] = fp8["TFLOP/s"]
+        result["fp8_gemm_frac_of_peak"] = fp8["roofline_frac"]
+
     result["cpu_baseline"] = cpu_baseline_w4a16(H, m, k, n, gs, args.cpu_budget)
     print(json.dumps(result), flush=True)
 

@@ -1,0 +1,470 @@
+// kernel-set (MI355X build) -- 8-bit MFMA GEMMs: fp8 blockwise-scaled and W8A8.
+//
+// Both take A [M,K] (K contiguous) and B [K,N] (N contiguous, the reference's
+// quantized-linear layout, gemm.h:79-98 / gemm.h:39-49 of cklxx/kernel-set).
+// MFMA wants both operands K-contiguous per lane, so each workgroup transposes
+// its B tile once while staging it into LDS (register byte transpose with
+// v_perm, then 32-bit LDS writes into a [n][k] layout); all four waves then read
+// MFMA fragments with 128-bit LDS loads. A tiles are copied to LDS unchanged.
+//
+// Tiling: workgroup 128x128 output tile, 4 waves as 2x2 of 64x64, K step 128.
+// Per K step each wave issues 4x4 MFMAs:
+//   fp8 : v_mfma_scale_f32_16x16x128_f8f6f4 (unit scales)        -> fp32
+//   int8: 2 x v_mfma_i32_16x16x64_i8                              -> int32
+// The next K step's global loads are issued into registers before the current
+// step's MFMAs (register double buffering) so HBM latency hides behind math.
+//
+// fp8 blockwise (gemm_fp8_blockwise.cu:107-161): inside one scale block of
+// block_k (a multiple of 128) the MFMA accumulates the raw fp32 partial P; at
+// the block end P is promoted: O = fma(P, a_s[m,kb] * b_s[kb,n/block_n], O).
+// W8A8 (gemm_w8a8.cu:120-142): exact int32 accumulation over all of K, then
+// v = (float(acc) * a_s) * b_s (+ bias), with no contraction of the multiplies.
+#include "kernel_set/gemm.h"
+#include "kernel_set/testing.h"
+#include "ks_common.hpp"
+
+namespace ks {
+namespace gemm8 {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+
+constexpr int kThreads = 256;
+constexpr int kBM = 128, kBN = 128, kBK = 128;
+constexpr int kLdsStride = kBK + 16;  // bytes per LDS row (16 B pad vs bank conflicts)
+
+enum Kind { FP8_E4M3 = 0, FP8_E5M2 = 1, INT8 = 2, INT8_RAW = 3 };
+
+// 4x4 byte transpose: in[r] holds bytes (r,0..3); out[c] holds bytes (0..3,c).
+__device__ inline void transpose4x4(const uint32_t in[4], uint32_t out[4]) {
+  // pair rows (0,1) and (2,3): interleave bytes
+  const uint32_t t01lo = __builtin_amdgcn_perm(in[1], in[0], 0x05010400u);  // r0c0 r1c0 r0c1 r1c1
+  const uint32_t t01hi = __builtin_amdgcn_perm(in[1], in[0], 0x07030602u);  // r0c2 r1c2 r0c3 r1c3
+  const uint32_t t23lo = __builtin_amdgcn_perm(in[3], in[2], 0x05010400u);
+  const uint32_t t23hi = __builtin_amdgcn_perm(in[3], in[2], 0x07030602u);
+  out[0] = __builtin_amdgcn_perm(t23lo, t01lo, 0x05040100u);  // c0: r0 r1 r2 r3
+  out[1] = __builtin_amdgcn_perm(t23lo, t01lo, 0x07060302u);
+  out[2] = __builtin_amdgcn_perm(t23hi, t01hi, 0x05040100u);
+  out[3] = __builtin_amdgcn_perm(t23hi, t01hi, 0x07060302u);
+}
+
+template <typename Out>
+__device__ inline void store_out(typename Out::storage* p, float v) {
+  *p = elem<Out>::from_f32(v);
+}
+
+struct Args {
+  void* out;
+  const uint8_t* a;
+  const uint8_t* b;
+  const float* a_scale;
+  const float* b_scale;
+  const void* bias;
+  int64_t m, n, k;
+  int block_n, block_k;    // fp8 blockwise
+  int64_t nkb, nnb;        // scale grid dims
+  int a_per_token, b_per_channel;  // w8a8
+};
+
+// Workgroup id -> (tile_m, tile_n). Tiles are walked column-major in groups so
+// that concurrently running workgroups share B column panels in L2.
+__device__ inline void tile_coords(int bid, int tiles_m, int tiles_n, int* tm, int* tn) {
+  constexpr int kGroup = 8;  // tile_m rows per group
+  const int per_group = kGroup * tiles_n;
+  const int g = bid / per_group;
+  const int first_m = g * kGroup;
+  const int gm = min(tiles_m - first_m, kGroup);
+  const int r = bid % per_group;
+  *tm = first_m + r % gm;
+  *tn = r / gm;
+}
+
+template <int KIND, typename Out>
+__global__ void __launch_bounds__(kThreads)
+gemm8_kernel(Args p) {
+  __shared__ __attribute__((aligned(16))) uint8_t sA[kBM * kLdsStride];
+  __shared__ __attribute__((aligned(16))) uint8_t sB[kBN * kLdsStride];  // [n][k]
+  __shared__ float sAs[kBM];
+  __shared__ float sBs[kBN];
+
+  const int tiles_m = static_cast<int>((p.m + kBM - 1) / kBM);
+  const int tiles_n = static_cast<int>((p.n + kBN - 1) / kBN);
+  int tm, tn;
+  tile_coords(blockIdx.x, tiles_m, tiles_n, &tm, &tn);
+  const int64_t m0 = static_cast<int64_t>(tm) * kBM;
+  const int64_t n0 = static_cast<int64_t>(tn) * kBN;
+
+  const int t = threadIdx.x;
+  const int lane = t % kWave;
+  const int wave = t / kWave;
+  const int wm = (wave / 2) * 64;  // wave tile origin inside the workgroup tile
+  const int wn = (wave % 2) * 64;
+
+  // ---- global -> register staging assignments ----
+  // A: 128 rows x 128 bytes = 1024 chunks of 16 B, 4 per thread.
+  // B: thread covers 4 k rows x 16 columns (4 chunks of 16 B).
+  const int b_cg = t % 8;   // 16-column group
+  const int b_kg = t / 8;   // 4-row group (0..31)
+  uint4 ra[4], rb[4];
+
+  auto load_tiles = [&](int64_t k0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = t + kThreads * i;
+      const int row = c / 8, kc = c % 8;
+      const int64_t gm = m0 + row, gk = k0 + 16 * kc;
+      ra[i] = (gm < p.m && gk < p.k)
+                  ? *reinterpret_cast<const uint4*>(p.a + gm * p.k + gk)
+                  : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t gk = k0 + 4 * b_kg + r, gn = n0 + 16 * b_cg;
+      rb[r] = (gk < p.k && gn < p.n)
+                  ? *reinterpret_cast<const uint4*>(p.b + gk * p.n + gn)
+                  : make_uint4(0, 0, 0, 0);
+    }
+  };
+
+  auto store_tiles = [&]() {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = t + kThreads * i;
+      const int row = c / 8, kc = c % 8;
+      *reinterpret_cast<uint4*>(sA + row * kLdsStride + 16 * kc) = ra[i];
+    }
+    const uint32_t d[4][4] = {{rb[0].x, rb[0].y, rb[0].z, rb[0].w},
+                              {rb[1].x, rb[1].y, rb[1].z, rb[1].w},
+                              {rb[2].x, rb[2].y, rb[2].z, rb[2].w},
+                              {rb[3].x, rb[3].y, rb[3].z, rb[3].w}};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t in[4] = {d[0][q], d[1][q], d[2][q], d[3][q]};
+      uint32_t o[4];
+      transpose4x4(in, o);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int col = 16 * b_cg + 4 * q + c;
+        *reinterpret_cast<uint32_t*>(sB + col * kLdsStride + 4 * b_kg) = o[c];
+      }
+    }
+  };
+
+  constexpr bool kFp8 = (KIND == FP8_E4M3 || KIND == FP8_E5M2);
+  // accumulators: 4x4 blocks of 16x16, 4 values per lane each
+  f32x4 acc_o[4][4];   // fp8: promoted output; unused for int8
+  f32x4 acc_p[4][4];   // fp8: raw partial of the current scale block
+  i32x4 acc_i[4][4];   // int8: exact accumulator
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      acc_o[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      acc_p[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      acc_i[i][j] = i32x4{0, 0, 0, 0};
+    }
+
+  const int li = lane % 16;       // row (A) / column (B) inside a 16-block
+  const int lk = lane / 16;       // k sub-slice
+  const int steps = static_cast<int>((p.k + kBK - 1) / kBK);
+  const int steps_per_block = kFp8 ? p.block_k / kBK : 1;
+
+  load_tiles(0);
+  for (int s = 0; s < steps; ++s) {
+    const int64_t k0 = static_cast<int64_t>(s) * kBK;
+    __syncthreads();  // previous step's LDS reads are done
+    store_tiles();
+    const bool promote = kFp8 && ((s + 1) % steps_per_block == 0 || s + 1 == steps);
+    if (kFp8 && promote) {
+      const int64_t kb = k0 / p.block_k;
+      if (t < kBM) {
+        const int64_t gm = m0 + t;
+        sAs[t] = gm < p.m ? p.a_scale[gm * p.nkb + kb] : 0.f;
+      } else {
+        const int64_t gn = n0 + (t - kBM);
+        sBs[t - kBM] = gn < p.n ? p.b_scale[kb * p.nnb + gn / p.block_n] : 0.f;
+      }
+    }
+    __syncthreads();
+    if (s + 1 < steps) load_tiles(k0 + kBK);  // in flight during the MFMAs
+
+    if constexpr (kFp8) {
+      i32x8 fa[4], fb[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint8_t* pa = sA + (wm + 16 * i + li) * kLdsStride + 32 * lk;
+        const uint4 x0 = *reinterpret_cast<const uint4*>(pa);
+        const uint4 x1 = *reinterpret_cast<const uint4*>(pa + 16);
+        fa[i] = i32x8{(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w,
+                      (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+        const uint8_t* pb = sB + (wn + 16 * i + li) * kLdsStride + 32 * lk;
+        const uint4 y0 = *reinterpret_cast<const uint4*>(pb);
+        const uint4 y1 = *reinterpret_cast<const uint4*>(pb + 16);
+        fb[i] = i32x8{(int)y0.x, (int)y0.y, (int)y0.z, (int)y0.w,
+                      (int)y1.x, (int)y1.y, (int)y1.z, (int)y1.w};
+      }
+      constexpr int fmt = (KIND == FP8_E5M2) ? 1 : 0;  // 0 = fp8 e4m3, 1 = bf8 e5m2
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc_p[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+              fa[i], fb[j], acc_p[i][j], fmt, fmt, 0, 127, 0, 127);
+      if (promote) {
+        // lane's output rows: wm + 16i + 4*lk + r ; column: wn + 16j + li
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float bs = sBs[wn + 16 * j + li];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const float sc = sAs[wm + 16 * i + 4 * lk + r] * bs;
+              acc_o[i][j][r] = fmaf(acc_p[i][j][r], sc, acc_o[i][j][r]);
+            }
+            acc_p[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        i32x4 fa[4], fb[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint4 x = *reinterpret_cast<const uint4*>(
+              sA + (wm + 16 * i + li) * kLdsStride + 64 * h + 16 * lk);
+          fa[i] = i32x4{(int)x.x, (int)x.y, (int)x.z, (int)x.w};
+          const uint4 y = *reinterpret_cast<const uint4*>(
+              sB + (wn + 16 * i + li) * kLdsStride + 64 * h + 16 * lk);
+          fb[i] = i32x4{(int)y.x, (int)y.y, (int)y.z, (int)y.w};
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc_i[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j], acc_i[i][j], 0, 0, 0);
+      }
+    }
+  }
+
+  // ---- epilogue ----
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t gn = n0 + wn + 16 * j + li;
+      if (gn >= p.n) continue;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t gm = m0 + wm + 16 * i + 4 * lk + r;
+        if (gm >= p.m) continue;
+        if constexpr (kFp8) {
+          store_out<Out>(static_cast<typename Out::storage*>(p.out) + gm * p.n + gn,
+                         acc_o[i][j][r]);
+        } else if constexpr (KIND == INT8_RAW) {
+          static_cast<int32_t*>(p.out)[gm * p.n + gn] = acc_i[i][j][r];
+        } else {
+          const float as = p.a_per_token ? p.a_scale[gm] : p.a_scale[0];
+          const float bs = p.b_per_channel ? p.b_scale[gn] : p.b_scale[0];
+          float v = __fmul_rn(__fmul_rn(static_cast<float>(acc_i[i][j][r]), as), bs);
+          if (p.bias)
+            v = __fadd_rn(v, elem<Out>::load(static_cast<const typename Out::storage*>(p.bias), gn));
+          store_out<Out>(static_cast<typename Out::storage*>(p.out) + gm * p.n + gn, v);
+        }
+      }
+    }
+}
+
+// Any-shape fp8 blockwise fallback (one thread per output, reference order).
+template <typename Dec, typename Out>
+__global__ void __launch_bounds__(kThreads)
+fp8_blockwise_simple_kernel(Args p) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (idx >= p.m * p.n) return;
+  const int64_t gm = idx / p.n, gn = idx % p.n;
+  float out = 0.f;
+  for (int64_t kb = 0; kb < p.nkb; ++kb) {
+    const int64_t k0 = kb * p.block_k;
+    const int64_t k1 = (k0 + p.block_k < p.k) ? k0 + p.block_k : p.k;
+    float part = 0.f;
+    for (int64_t kk = k0; kk < k1; ++kk)
+      part = fmaf(Dec::dec(p.a[gm * p.k + kk]), Dec::dec(p.b[kk * p.n + gn]), part);
+    out = fmaf(part, p.a_scale[gm * p.nkb + kb] * p.b_scale[kb * p.nnb + gn / p.block_n], out);
+  }
+  store_out<Out>(static_cast<typename Out::storage*>(p.out) + idx, out);
+}
+
+// Any-shape W8A8 fallback.
+template <int KIND, typename Out>
+__global__ void __launch_bounds__(kThreads)
+w8a8_simple_kernel(Args p) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (idx >= p.m * p.n) return;
+  const int64_t gm = idx / p.n, gn = idx % p.n;
+  const int8_t* a = reinterpret_cast<const int8_t*>(p.a);
+  const int8_t* b = reinterpret_cast<const int8_t*>(p.b);
+  int32_t acc = 0;
+  for (int64_t kk = 0; kk < p.k; ++kk) acc += static_cast<int32_t>(a[gm * p.k + kk]) * b[kk * p.n + gn];
+  if constexpr (KIND == INT8_RAW) {
+    static_cast<int32_t*>(p.out)[idx] = acc;
+  } else {
+    const float as = p.a_per_token ? p.a_scale[gm] : p.a_scale[0];
+    const float bs = p.b_per_channel ? p.b_scale[gn] : p.b_scale[0];
+    float v = __fmul_rn(__fmul_rn(static_cast<float>(acc), as), bs);
+    if (p.bias) v = __fadd_rn(v, elem<Out>::load(static_cast<const typename Out::storage*>(p.bias), gn));
+    store_out<Out>(static_cast<typename Out::storage*>(p.out) + idx, v);
+  }
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline bool tiled_ok(const Args& p) {
+  return p.k % 16 == 0 && p.n % 16 == 0 && aligned16(p.a) && aligned16(p.b) &&
+         p.m < (int64_t{1} << 31) && p.n < (int64_t{1} << 31);
+}
+
+template <int KIND, typename Out>
+void launch_tiled(const Args& p, hipStream_t s) {
+  const int64_t tiles = ((p.m + kBM - 1) / kBM) * ((p.n + kBN - 1) / kBN);
+  hipLaunchKernelGGL((gemm8_kernel<KIND, Out>), dim3(static_cast<unsigned>(tiles)),
+                     dim3(kThreads), 0, s, p);
+}
+
+inline unsigned simple_grid(const Args& p) {
+  return static_cast<unsigned>((p.m * p.n + kThreads - 1) / kThreads);
+}
+
+template <typename Out>
+void run_fp8(const Args& p, ks_dtype_t fp8, hipStream_t s) {
+  const bool tiled = tiled_ok(p) && p.block_k % kBK == 0;
+  if (fp8 == KS_DTYPE_F8E4M3) {
+    if (tiled) launch_tiled<FP8_E4M3, Out>(p, s);
+    else hipLaunchKernelGGL((fp8_blockwise_simple_kernel<e4m3_t, Out>), dim3(simple_grid(p)), dim3(kThreads), 0, s, p);
+  } else {
+    if (tiled) launch_tiled<FP8_E5M2, Out>(p, s);
+    else hipLaunchKernelGGL((fp8_blockwise_simple_kernel<e5m2_t, Out>), dim3(simple_grid(p)), dim3(kThreads), 0, s, p);
+  }
+}
+
+template <int KIND, typename Out>
+void run_w8a8(const Args& p, hipStream_t s) {
+  if (tiled_ok(p)) launch_tiled<KIND, Out>(p, s);
+  else hipLaunchKernelGGL((w8a8_simple_kernel<KIND, Out>), dim3(simple_grid(p)), dim3(kThreads), 0, s, p);
+}
+
+}  // namespace gemm8
+}  // namespace ks
+
+using namespace ks;
+using namespace ks::gemm8;
+
+namespace {
+constexpr int64_t kI64Max = 9223372036854775807LL;
+bool mul_overflows(int64_t a, int64_t b) { return a > kI64Max / b; }
+constexpr int64_t kMaxTiles = 2147483647LL;
+}  // namespace
+
+extern "C" {
+
+ks_status_t ks_gemm_fp8_blockwise(void* out, const void* a_fp8, const void* b_fp8,
+                                  const float* a_scale, const float* b_scale, int64_t m,
+                                  int64_t n, int64_t k, int block_n, int block_k,
+                                  ks_dtype_t fp8_dtype, ks_dtype_t out_dtype,
+                                  ks_stream_t stream) {
+  KS_REQUIRE_PTR(out);
+  KS_REQUIRE_PTR(a_fp8);
+  KS_REQUIRE_PTR(b_fp8);
+  KS_REQUIRE_PTR(a_scale);
+  KS_REQUIRE_PTR(b_scale);
+  if (m <= 0 || n <= 0 || k <= 0) KS_FAIL(KS_ERROR_INVALID_ARGUMENT, "ks_gemm_fp8_blockwise: bad shape");
+  if (block_n <= 0 || block_k <= 0)
+    KS_FAIL(KS_ERROR_INVALID_ARGUMENT, "ks_gemm_fp8_blockwise: block_n/block_k must be > 0");
+  if (mul_overflows(m, k) || mul_overflows(k, n) || mul_overflows(m, n))
+    KS_FAIL(KS_ERROR_UNSUPPORTED_SHAPE, "ks_gemm_fp8_blockwise: M*K / K*N / M*N exceeds int64 range");
+  if (fp8_dtype != KS_DTYPE_F8E4M3 && fp8_dtype != KS_DTYPE_F8E5M2)
+    KS_FAIL(KS_ERROR_UNSUPPORTED_DTYPE, "ks_gemm_fp8_blockwise: fp8_dtype must be e4m3 or e5m2");
+  if (out_dtype != KS_DTYPE_F32 && out_dtype != KS_DTYPE_F16 && out_dtype != KS_DTYPE_BF16)
+    KS_FAIL(KS_ERROR_UNSUPPORTED_DTYPE, "ks_gemm_fp8_blockwise: out_dtype must be f32/f16/bf16");
+  if (((m + kBM - 1) / kBM) > kMaxTiles / ((n + kBN - 1) / kBN) || m * n / kThreads >= kMaxTiles)
+    KS_FAIL(KS_ERROR_UNSUPPORTED_SHAPE, "ks_gemm_fp8_blockwise: tile grid exceeds grid limits");
+  Args p{};
+  p.out = out;
+  p.a = static_cast<const uint8_t*>(a_fp8);
+  p.b = static_cast<const uint8_t*>(b_fp8);
+  p.a_scale = a_scale;
+  p.b_scale = b_scale;
+  p.m = m; p.n = n; p.k = k;
+  p.block_n = block_n; p.block_k = block_k;
+  p.nkb = (k + block_k - 1) / block_k;
+  p.nnb = (n + block_n - 1) / block_n;
+  auto s = to_stream(stream);
+  switch (out_dtype) {
+    case KS_DTYPE_F32: run_fp8<f32_t>(p, fp8_dtype, s); break;
+    case KS_DTYPE_F16: run_fp8<f16_t>(p, fp8_dtype, s); break;
+    default: run_fp8<bf16_t>(p, fp8_dtype, s); break;
+  }
+  KS_LAUNCH_STATUS("ks_gemm_fp8_blockwise");
+  return KS_SUCCESS;
+}
+
+ks_status_t ks_gemm_w8a8(void* c, const void* a_i8, const void* b_i8, const float* a_scale,
+                         const float* b_scale, const void* bias, int64_t m, int64_t n,
+                         int64_t k, ks_quant_mode_t a_mode, ks_quant_mode_t b_mode,
+                         ks_dtype_t out_dtype, ks_stream_t stream) {
+  KS_REQUIRE_PTR(c);
+  KS_REQUIRE_PTR(a_i8);
+  KS_REQUIRE_PTR(b_i8);
+  KS_REQUIRE_PTR(a_scale);
+  KS_REQUIRE_PTR(b_scale);
+  if (m <= 0 || n <= 0 || k <= 0) KS_FAIL(KS_ERROR_INVALID_ARGUMENT, "ks_gemm_w8a8: bad shape");
+  if (a_mode != KS_QUANT_PER_TENSOR && a_mode != KS_QUANT_PER_TOKEN)
+    KS_FAIL(KS_ERROR_INVALID_ARGUMENT, "ks_gemm_w8a8: a_mode must be per-tensor or per-token");
+  if (b_mode != KS_QUANT_PER_TENSOR && b_mode != KS_QUANT_PER_CHANNEL)
+    KS_FAIL(KS_ERROR_INVALID_ARGUMENT, "ks_gemm_w8a8: b_mode must be per-tensor or per-channel");
+  if (out_dtype != KS_DTYPE_F32 && out_dtype != KS_DTYPE_F16 && out_dtype != KS_DTYPE_BF16)
+    KS_FAIL(KS_ERROR_UNSUPPORTED_DTYPE, "ks_gemm_w8a8: out_dtype must be f32/f16/bf16");
+  if (mul_overflows(m, k) || mul_overflows(k, n) || mul_overflows(m, n) || m * n / kThreads >= kMaxTiles)
+    KS_FAIL(KS_ERROR_UNSUPPORTED_SHAPE, "ks_gemm_w8a8: shape exceeds grid limits");
+  if (k > 260000)  // 127*127*k must stay below 2^31 for exact int32 accumulation
+    KS_FAIL(KS_ERROR_UNSUPPORTED_SHAPE, "ks_gemm_w8a8: K too large for exact int32 accumulation");
+  Args p{};
+  p.out = c;
+  p.a = static_cast<const uint8_t*>(a_i8);
+  p.b = static_cast<const uint8_t*>(b_i8);
+  p.a_scale = a_scale;
+  p.b_scale = b_scale;
+  p.bias = bias;
+  p.m = m; p.n = n; p.k = k;
+  p.a_per_token = a_mode == KS_QUANT_PER_TOKEN;
+  p.b_per_channel = b_mode == KS_QUANT_PER_CHANNEL;
+  auto s = to_stream(stream);
+  switch (out_dtype) {
+    case KS_DTYPE_F32: run_w8a8<INT8, f32_t>(p, s); break;
+    case KS_DTYPE_F16: run_w8a8<INT8, f16_t>(p, s); break;
+    default: run_w8a8<INT8, bf16_t>(p, s); break;
+  }
+  KS_LAUNCH_STATUS("ks_gemm_w8a8");
+  return KS_SUCCESS;
+}
+
+ks_status_t ks_testing_gemm_w8a8_i32(int32_t* acc, const void* a_i8, const void* b_i8,
+                                     int64_t m, int64_t n, int64_t k, ks_stream_t stream) {
+  KS_REQUIRE_PTR(acc);
+  KS_REQUIRE_PTR(a_i8);
+  KS_REQUIRE_PTR(b_i8);
+  if (m <= 0 || n <= 0 || k <= 0) KS_FAIL(KS_ERROR_INVALID_ARGUMENT, "ks_testing_gemm_w8a8_i32: bad shape");
+  if (mul_overflows(m, k) || mul_overflows(k, n) || mul_overflows(m, n) || m * n / kThreads >= kMaxTiles)
+    KS_FAIL(KS_ERROR_UNSUPPORTED_SHAPE, "ks_testing_gemm_w8a8_i32: shape exceeds grid limits");
+  Args p{};
+  p.out = acc;
+  p.a = static_cast<const uint8_t*>(a_i8);
+  p.b = static_cast<const uint8_t*>(b_i8);
+  p.m = m; p.n = n; p.k = k;
+  run_w8a8<INT8_RAW, f32_t>(p, to_stream(stream));
+  KS_LAUNCH_STATUS("ks_testing_gemm_w8a8_i32");
+  return KS_SUCCESS;
+}
+
+}  // extern "C"

@@ -17,8 +17,15 @@
 // across the S splits by the last workgroup to arrive at that column tile
 // (fixed summation order, so results are deterministic). Split workgroups of
 // one tile are mapped to the same XCD so the partials stay in one L2.
+//
+// Batched path (M > 8): MFMA, see w4a16_mfma.hpp. Workgroups own 64 columns x
+// a range of quantization groups; K splits across workgroups are reduced by the
+// last arrival exactly like the decode path.
+#include <algorithm>
+
 #include "kernel_set/gemm.h"
 #include "ks_common.hpp"
+#include "w4a16_mfma.hpp"
 #include "workspace.hpp"
 
 namespace ks {
@@ -227,6 +234,106 @@ simple_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
   c[m * n + col] = elem<T>::from_f32(acc);
 }
 
+
+// ---------------------------------------------------------------------------
+// Batched MFMA path.
+// ---------------------------------------------------------------------------
+template <typename T, int MB>
+__global__ void __launch_bounds__(w4mma::kThreads)
+mfma_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
+            const uint8_t* __restrict__ b, const uint16_t* __restrict__ scales,
+            const uint16_t* __restrict__ zeros, const uint16_t* __restrict__ bias,
+            int64_t row0, int64_t row1, int64_t n, int64_t k, int gs, int splits,
+            int groups_per_split, float* __restrict__ ws, unsigned* __restrict__ counters) {
+  constexpr int kRows = 16 * MB;
+  constexpr int kPlane = kRows * w4mma::kTileN;
+  __shared__ float red[4 * kPlane];
+  __shared__ int last_flag;
+  int tile, split;
+  map_tile(blockIdx.x, gridDim.x, splits, &tile, &split);
+  const int ng = static_cast<int>(k / gs);
+  w4mma::TileArgs p;
+  p.a = a; p.b = b; p.s = scales; p.z = zeros;
+  p.row0 = row0; p.row1 = row1; p.n = n; p.k = k; p.gs = gs;
+  p.n0 = static_cast<int64_t>(tile) * w4mma::kTileN;
+  p.g_begin = split * groups_per_split;
+  p.g_end = min(p.g_begin + groups_per_split, ng);
+  w4mma::tile_partial<T, MB>(p, row0, red);
+  const float* res = red + 3 * kPlane;
+  const int t = threadIdx.x;
+  const int64_t rows = row1 - row0;
+  if (splits == 1) {
+    for (int e = t; e < kPlane; e += w4mma::kThreads) {
+      const int64_t r = e / w4mma::kTileN, col = p.n0 + e % w4mma::kTileN;
+      if (r >= rows || col >= n) continue;
+      float o = res[e];
+      if (bias) o += h2f<T>(bias[col]);
+      c[(row0 + r) * n + col] = elem<T>::from_f32(o);
+    }
+    return;
+  }
+  for (int e = t; e < kPlane; e += w4mma::kThreads) {
+    const int64_t r = e / w4mma::kTileN, col = p.n0 + e % w4mma::kTileN;
+    if (r >= rows || col >= n) continue;
+    ws[(static_cast<int64_t>(split) * rows + r) * n + col] = res[e];
+  }
+  __threadfence();
+  __syncthreads();
+  if (t == 0) {
+    const unsigned prev = atomicAdd(&counters[tile], 1u);
+    last_flag = (prev == static_cast<unsigned>(splits - 1));
+  }
+  __syncthreads();
+  if (!last_flag) return;
+  __threadfence();
+  for (int e = t; e < kPlane; e += w4mma::kThreads) {
+    const int64_t r = e / w4mma::kTileN, col = p.n0 + e % w4mma::kTileN;
+    if (r >= rows || col >= n) continue;
+    float o = 0.f;
+    for (int sp = 0; sp < splits; ++sp) o += ws[(static_cast<int64_t>(sp) * rows + r) * n + col];
+    if (bias) o += h2f<T>(bias[col]);
+    c[(row0 + r) * n + col] = elem<T>::from_f32(o);
+  }
+  if (t == 0) counters[tile] = 0u;
+}
+
+template <typename T, int MB>
+void launch_mfma(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_t* s,
+                 const uint16_t* z, const uint16_t* bias, int64_t r0, int64_t r1, int64_t n,
+                 int64_t k, int gs, int tiles, int splits, int gps, const Scratch& sc,
+                 hipStream_t st) {
+  hipLaunchKernelGGL((mfma_kernel<T, MB>), dim3(tiles * splits), dim3(w4mma::kThreads), 0, st,
+                     c, a, b, s, z, bias, r0, r1, n, k, gs, splits, gps, sc.partial,
+                     sc.counters);
+}
+
+template <typename T>
+ks_status_t run_mfma(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_t* s,
+                     const uint16_t* z, const uint16_t* bias, int64_t m, int64_t n, int64_t k,
+                     int gs, hipStream_t st) {
+  const int tiles = static_cast<int>((n + w4mma::kTileN - 1) / w4mma::kTileN);
+  const int ng = static_cast<int>(k / gs);
+  // Aim for ~1024 workgroups but keep >= 4 groups (one per wave) per split.
+  int splits = (1024 + tiles - 1) / tiles;
+  splits = std::max(1, std::min(splits, ng / 4));
+  const int gps = (ng + splits - 1) / splits;
+  splits = (ng + gps - 1) / gps;
+  const int mb_rows = m >= 64 ? 64 : (m > 16 ? 32 : 16);
+  Scratch sc;
+  if (splits > 1) {
+    ks_status_t r = get_scratch(st, static_cast<size_t>(splits) * mb_rows * n,
+                                static_cast<size_t>(tiles), &sc, "ks_gemm_w4a16");
+    if (r != KS_SUCCESS) return r;
+  }
+  for (int64_t r0 = 0; r0 < m; r0 += mb_rows) {
+    const int64_t r1 = std::min(m, r0 + mb_rows);
+    if (mb_rows == 64) launch_mfma<T, 4>(c, a, b, s, z, bias, r0, r1, n, k, gs, tiles, splits, gps, sc, st);
+    else if (mb_rows == 32) launch_mfma<T, 2>(c, a, b, s, z, bias, r0, r1, n, k, gs, tiles, splits, gps, sc, st);
+    else launch_mfma<T, 1>(c, a, b, s, z, bias, r0, r1, n, k, gs, tiles, splits, gps, sc, st);
+  }
+  return KS_SUCCESS;
+}
+
 inline bool aligned(const void* p, uintptr_t q) {
   return p == nullptr || (reinterpret_cast<uintptr_t>(p) % q) == 0;
 }
@@ -259,6 +366,9 @@ ks_status_t run(void* c_, const void* a_, const void* b_, const void* s_, const 
   const auto* z = static_cast<const uint16_t*>(z_);
   const auto* bias = static_cast<const uint16_t*>(bias_);
 
+  const bool mfma = m > kMaxGemvM && (gs % 32 == 0) && (n % 4 == 0) && aligned(a, 16) &&
+                    aligned(s, 8) && aligned(z, 8) && aligned(b, 4);
+  if (mfma) return run_mfma<T>(c, a, b, s, z, bias, m, n, k, gs, st);
   const bool vec = (n % 16 == 0) && (gs % 16 == 0) && n <= (int64_t{1} << 30) &&
                    k <= (int64_t{1} << 30) && aligned(b, 16) && aligned(s, 16) &&
                    aligned(z, 16) && aligned(a, 4);

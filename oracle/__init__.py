@@ -340,3 +340,46 @@ def rel_err(out, ref) -> float:
     r = np.asarray(ref, np.float64)
     denom = max(float(np.abs(r).max()) if r.size else 0.0, 1e-6)
     return float(np.abs(o - r).max()) / denom if r.size else 0.0
+
+
+# ---------------------------------------------------------------------------
+# MoE routing helpers (fixture construction for the grouped GEMM)
+# ---------------------------------------------------------------------------
+def moe_topk_ids(logits, top_k: int) -> np.ndarray:
+    """Top-k experts per token (moe_gate.cu:88-105): softmax is monotonic, so
+    the selection is the k largest logits, the lowest expert id winning ties."""
+    lg = _c(logits, np.float32)
+    order = np.argsort(-lg, axis=1, kind="stable")  # stable: lower id first on ties
+    return order[:, :top_k].astype(np.int32)
+
+
+def moe_group_rows(ids, num_experts: int, pad: int = 1):
+    """Rows grouped by expert for the grouped GEMM (moe_permute.cu:57-101 with a
+    fixed intra-expert order: increasing (token, slot)). Each expert's block is
+    padded to a multiple of `pad` rows. Returns (row_src, offsets): row_src[r] is
+    the flat (token*top_k + slot) index feeding row r, or -1 for padding;
+    offsets is int32 [E+1] over the padded rows."""
+    flat = _c(ids, np.int32).reshape(-1)
+    rows, offs = [], [0]
+    for e in range(num_experts):
+        src = np.nonzero(flat == e)[0]
+        padded = -(-len(src) // pad) * pad
+        rows.append(np.concatenate([src, np.full(padded - len(src), -1)]))
+        offs.append(offs[-1] + padded)
+    return np.concatenate(rows).astype(np.int64), np.array(offs, np.int32)
+
+
+def moe_w4a16_ref(a, b_packed, scales, zeros, offsets, group_size, dtype="bf16"):
+    """Per expert e: C[off_e:off_{e+1}] = A[off_e:off_{e+1}] @ dequant(B_e)
+    (moe_grouped_gemm.cu:99-124 composed with bench.py:1274-1285), fp32."""
+    a = _c(a, np.float32)
+    E = len(offsets) - 1
+    n = b_packed.shape[2]
+    out = np.zeros((a.shape[0], n), np.float32)
+    for e in range(E):
+        r0, r1 = int(offsets[e]), int(offsets[e + 1])
+        if r1 > r0:
+            w = w4a16_dequant_weight(b_packed[e], scales[e],
+                                     None if zeros is None else zeros[e], group_size, dtype)
+            out[r0:r1] = a[r0:r1] @ w
+    return out

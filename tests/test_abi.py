@@ -68,7 +68,7 @@ def test_runtime_introspection():
     assert L.ks_status_string(99) == b"KS_ERROR_UNKNOWN"
     assert [L.ks_dtype_size_bits(d) for d in range(11)] == [32, 16, 16, 8, 8, 64, 64, 32, 8, 8, 4]
     assert L.ks_dtype_name(DType.BF16) == b"bf16" and L.ks_dtype_name(99) == b"unknown"
-    assert ctypes.sizeof(_lib.ks_device_properties_t) == 256 + 6 * 4 + 4 + 8 + 3 * 4 + 4
+    assert ctypes.sizeof(_lib.ks_device_properties_t) == 256 + 6 * 4 + 8 + 3 * 4 + 4  # trailing pad to 8
 
 
 def _status(fn, *args):
