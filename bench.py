@@ -52,9 +52,14 @@ class Timer:
         self.torch = torch
         self.stream = torch.cuda.Stream()
 
-    def run(self, fn, per_graph, steps, warmup):
-        """fn(i) issues call i (i < per_graph). Returns (ms per call, calls timed)."""
+    def run(self, fn, rotate, steps, warmup, min_per_graph=64):
+        """fn(i) issues call i on buffer set i (i < rotate). Each graph holds at
+        least `min_per_graph` calls so graph-launch overhead is amortized.
+        Returns (ms per call, calls timed)."""
         torch = self.torch
+        per_graph = max(rotate, min_per_graph)
+        inner = fn
+        fn = lambda i: inner(i % rotate)  # noqa: E731
         with torch.cuda.stream(self.stream):
             for i in range(per_graph):  # eager warm-up: allocates library scratch
                 fn(i)

@@ -6,21 +6,25 @@
 //   low nibble), scales/zeros/A/C/bias all in the activation dtype, fp32 math,
 //   output rounded to nearest even.
 //
-// Decode path (M <= 8): HBM-bound. Every byte of the 4-bit weight stream is
-// read exactly once with 16-byte loads; a workgroup covers 128 columns (one
-// 128-byte line per packed row) by 32*RPT packed rows, so the grid is
-// (N/128) column tiles x S K-splits and fills all 256 CUs even at N = 4096.
-// Each thread owns 16 columns x 2*RPT consecutive k of one quantization group,
-// so the group's scale/zero are applied once per thread:
-//   sum_k a_k (q_k - z) s = s * (sum_k a_k q_k - z * sum_k a_k).
-// Partials are reduced with wave shuffles and LDS inside the workgroup, then
-// across the S splits by the last workgroup to arrive at that column tile
-// (fixed summation order, so results are deterministic). Split workgroups of
-// one tile are mapped to the same XCD so the partials stay in one L2.
+// Decode path (M <= 8), HBM-bound. Measured on MI355X: reading the weight
+// stream reaches full bandwidth only when each workgroup reads whole 128-byte
+// lines of consecutive packed rows (column strips narrower than a line read
+// ~2x slower), so a workgroup owns a 128-column x 32*RPT-row tile and K is
+// split over S workgroups. Cross-workgroup reduction inside one kernel needs an
+// agent-scope release (an L2 writeback per workgroup on this chip), which
+// costs more than a second launch, so the split partials go to a scratch plane
+// and a small reduce kernel sums them in a fixed order (deterministic) and
+// adds the bias.
 //
-// Batched path (M > 8): MFMA, see w4a16_mfma.hpp. Workgroups own 64 columns x
-// a range of quantization groups; K splits across workgroups are reduced by the
-// last arrival exactly like the decode path.
+// Inner loop: v_dot2_f32_bf16 (or _f16). The activation pair (a[2kp],
+// a[2kp+1]) is used as loaded; each packed byte becomes the 16-bit float pair
+// (base + q_even, base + q_odd) with two v_perm ops per 4 columns
+// (bf16 0x4300|q = 128 + q; f16 0x5800|q = 128 + q/8, both exact), so
+//   sum_k a_k * w_k = s * (u * (D - (128 + z/u) * sum_k a_k)),  u = 1 or 8,
+// where D is the dot2 accumulator; each thread's 2*RPT k lie in one group.
+//
+// Batched path (M > 8): bf16/f16 MFMA, see w4a16_mfma.hpp, with the same
+// split-plane + reduce scheme when K is split.
 #include <algorithm>
 
 #include "kernel_set/gemm.h"
@@ -34,28 +38,42 @@ namespace w4a16 {
 constexpr int kThreads = 256;
 constexpr int kLanesN = 8;                    // lanes across the column tile
 constexpr int kTileN = kLanesN * 16;          // 128 columns per workgroup
-constexpr int kRowsPar = kThreads / kLanesN;  // 32 packed rows in flight
+constexpr int kRowsPar = kThreads / kLanesN;  // 32 row lanes
 constexpr int kMaxGemvM = 8;
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+template <typename T>
+struct dot;
+
+template <>
+struct dot<bf16_t> {
+  static constexpr uint32_t base_byte = 0x43434343u;  // 0x43xx = bf16 128 + low 7 bits
+  static constexpr uint32_t ones = 0x3f803f80u;
+  static constexpr float unit = 1.0f;
+  __device__ static inline float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a),
+                                           __builtin_bit_cast(bf16x2, b), c, false);
+  }
+};
+
+template <>
+struct dot<f16_t> {
+  static constexpr uint32_t base_byte = 0x58585858u;  // 0x58xx = f16 128 + xx/8
+  static constexpr uint32_t ones = 0x3c003c00u;
+  static constexpr float unit = 0.125f;
+  __device__ static inline float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c,
+                                  false);
+  }
+};
 
 template <typename T>
 __device__ inline float h2f(uint16_t h) { return elem<T>::to_f32(h); }
 
-// 16 consecutive 16-bit values as fp32.
-template <typename T>
-__device__ inline void load16h(const uint16_t* p, float v[16]) {
-  const uint4 a = *reinterpret_cast<const uint4*>(p);
-  const uint4 b = *reinterpret_cast<const uint4*>(p + 8);
-  const uint32_t d[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    v[2 * i] = h2f<T>(static_cast<uint16_t>(d[i] & 0xffffu));
-    v[2 * i + 1] = h2f<T>(static_cast<uint16_t>(d[i] >> 16));
-  }
-}
-
-// Workgroup id -> (column tile, k split). When the grid divides into the 8
-// XCDs, consecutive logical ids land on one XCD (hardware dispatches ids
-// round-robin over XCDs), so the S splits of a tile share an L2.
+// Workgroup id -> (column tile, k split); splits of one tile share an XCD
+// when the grid divides into the 8 XCDs (ids are dispatched round-robin).
 __device__ inline void map_tile(int bid, int nblocks, int splits, int* tile, int* split) {
   int logical = bid;
   if ((nblocks & 7) == 0) logical = (bid & 7) * (nblocks >> 3) + (bid >> 3);
@@ -63,15 +81,35 @@ __device__ inline void map_tile(int bid, int nblocks, int splits, int* tile, int
   *split = logical % splits;
 }
 
+// acc[m][c0..c0+3] += a_pair[m] . (base + q) for the 4 columns in packed dword d.
+template <typename T, int MT>
+__device__ inline void dword_dot(uint32_t d, const uint32_t (&ap)[MT], float (*acc)[16], int c0) {
+  const uint32_t lo = d & 0x0f0f0f0fu, hi = (d >> 4) & 0x0f0f0f0fu;
+  const uint32_t x0 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);  // lo0 hi0 lo1 hi1
+  const uint32_t x1 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);  // lo2 hi2 lo3 hi3
+  constexpr uint32_t B = dot<T>::base_byte;
+  const uint32_t w0 = __builtin_amdgcn_perm(B, x0, 0x04010400u);  // (base|lo0, base|hi0)
+  const uint32_t w1 = __builtin_amdgcn_perm(B, x0, 0x04030402u);
+  const uint32_t w2 = __builtin_amdgcn_perm(B, x1, 0x04010400u);
+  const uint32_t w3 = __builtin_amdgcn_perm(B, x1, 0x04030402u);
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    acc[m][c0 + 0] = dot<T>::dot2(ap[m], w0, acc[m][c0 + 0]);
+    acc[m][c0 + 1] = dot<T>::dot2(ap[m], w1, acc[m][c0 + 1]);
+    acc[m][c0 + 2] = dot<T>::dot2(ap[m], w2, acc[m][c0 + 2]);
+    acc[m][c0 + 3] = dot<T>::dot2(ap[m], w3, acc[m][c0 + 3]);
+  }
+}
+
+// Partial GEMV over one (128-column, 32*RPT-packed-row) tile for MT <= 8 rows.
+// splits == 1: writes C (+bias) directly; else writes ws[split][m][n].
 template <typename T, int MT, int RPT>
 __global__ void __launch_bounds__(kThreads)
 gemv_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
             const uint8_t* __restrict__ b, const uint16_t* __restrict__ scales,
             const uint16_t* __restrict__ zeros, const uint16_t* __restrict__ bias,
-            int m_rows, int n, int k, int gs, int splits, float* __restrict__ ws,
-            unsigned* __restrict__ counters) {
-  __shared__ float red[kThreads / kWave][MT][kTileN];
-  __shared__ int last_flag;
+            int m_rows, int n, int k, int gs, int splits, float* __restrict__ ws) {
+  __shared__ float red[kRowsPar][kTileN + 4];
 
   int tile, split;
   map_tile(blockIdx.x, gridDim.x, splits, &tile, &split);
@@ -83,19 +121,29 @@ gemv_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
   const bool live = (col0 < n) && (kp0 < k / 2);
 
   float part[MT][16];
-#pragma unroll
-  for (int m = 0; m < MT; ++m)
-#pragma unroll
-    for (int j = 0; j < 16; ++j) part[m][j] = 0.f;
-
   if (live) {
+    // Issue every load of this thread before any math: weights (streamed),
+    // activation pairs, then this group's scales and zeros.
     uint4 w[RPT];
 #pragma unroll
-    for (int i = 0; i < RPT; ++i)
-      w[i] = load_stream16(b + static_cast<int64_t>(kp0 + i) * n + col0);
+    for (int i = 0; i < RPT; ++i) w[i] = load_stream16(b + static_cast<int64_t>(kp0 + i) * n + col0);
+    uint32_t ap[RPT][MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      const uint32_t* arow = reinterpret_cast<const uint32_t*>(a + static_cast<int64_t>(m) * k) + kp0;
+#pragma unroll
+      for (int i = 0; i < RPT; ++i) ap[i][m] = (m < m_rows) ? arow[i] : 0u;
+    }
+    const int64_t g = static_cast<int64_t>(2 * kp0 / gs) * n + col0;
+    const uint4 s0 = *reinterpret_cast<const uint4*>(scales + g);
+    const uint4 s1 = *reinterpret_cast<const uint4*>(scales + g + 8);
+    uint4 z0 = make_uint4(0, 0, 0, 0), z1 = make_uint4(0, 0, 0, 0);
+    if (zeros) {
+      z0 = *reinterpret_cast<const uint4*>(zeros + g);
+      z1 = *reinterpret_cast<const uint4*>(zeros + g + 8);
+    }
 
-    float acc[MT][16];
-    float asum[MT];
+    float acc[MT][16], asum[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
       asum[m] = 0.f;
@@ -104,109 +152,78 @@ gemv_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
     }
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
-      float a_lo[MT], a_hi[MT];
 #pragma unroll
-      for (int m = 0; m < MT; ++m) {
-        if (m < m_rows) {
-          const uint32_t pr = *reinterpret_cast<const uint32_t*>(
-              a + static_cast<int64_t>(m) * k + 2 * (kp0 + i));
-          a_lo[m] = h2f<T>(static_cast<uint16_t>(pr & 0xffffu));
-          a_hi[m] = h2f<T>(static_cast<uint16_t>(pr >> 16));
-        } else {
-          a_lo[m] = 0.f;
-          a_hi[m] = 0.f;
-        }
-        asum[m] += a_lo[m] + a_hi[m];
-      }
-      const uint32_t d[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint32_t lo = d[q] & 0x0f0f0f0fu;
-        const uint32_t hi = (d[q] >> 4) & 0x0f0f0f0fu;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float ql = static_cast<float>((lo >> (8 * j)) & 0xffu);
-          const float qh = static_cast<float>((hi >> (8 * j)) & 0xffu);
-#pragma unroll
-          for (int m = 0; m < MT; ++m) {
-            acc[m][4 * q + j] = fmaf(a_lo[m], ql, acc[m][4 * q + j]);
-            acc[m][4 * q + j] = fmaf(a_hi[m], qh, acc[m][4 * q + j]);
-          }
-        }
-      }
+      for (int m = 0; m < MT; ++m) asum[m] = dot<T>::dot2(ap[i][m], dot<T>::ones, asum[m]);
+      dword_dot<T, MT>(w[i].x, ap[i], acc, 0);
+      dword_dot<T, MT>(w[i].y, ap[i], acc, 4);
+      dword_dot<T, MT>(w[i].z, ap[i], acc, 8);
+      dword_dot<T, MT>(w[i].w, ap[i], acc, 12);
     }
-    // All 2*RPT k of this thread share one group (gs is a multiple of 2*RPT).
-    const int64_t g = static_cast<int64_t>(2 * kp0 / gs) * n + col0;
-    float s[16], z[16];
-    load16h<T>(scales + g, s);
-    if (zeros) {
-      load16h<T>(zeros + g, z);
-    } else {
-#pragma unroll
-      for (int j = 0; j < 16; ++j) z[j] = 0.f;
-    }
-#pragma unroll
-    for (int m = 0; m < MT; ++m)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) part[m][j] = s[j] * fmaf(-z[j], asum[m], acc[m][j]);
-  }
-
-  // Reduce over the 8 row blocks inside a wave (lane bits 3..5) ...
-#pragma unroll
-  for (int m = 0; m < MT; ++m)
+    const uint32_t sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    const uint32_t zv[8] = {z0.x, z0.y, z0.z, z0.w, z1.x, z1.y, z1.z, z1.w};
+    constexpr float u = dot<T>::unit;
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      float v = part[m][j];
-      v += __shfl_xor(v, 8, 64);
-      v += __shfl_xor(v, 16, 64);
-      v += __shfl_xor(v, 32, 64);
-      part[m][j] = v;
+      const float sj = h2f<T>(static_cast<uint16_t>(sv[j / 2] >> (16 * (j & 1))));
+      const float zj = h2f<T>(static_cast<uint16_t>(zv[j / 2] >> (16 * (j & 1))));
+      const float cj = 128.0f + zj * u;  // zero-point in the base+q*u encoding
+      const float se = sj * (1.0f / u);
+#pragma unroll
+      for (int m = 0; m < MT; ++m) part[m][j] = se * fmaf(-cj, asum[m], acc[m][j]);
     }
-  const int wave = t / kWave;
-  if ((t % kWave) < kLanesN) {
+  } else {
 #pragma unroll
     for (int m = 0; m < MT; ++m)
 #pragma unroll
-      for (int j = 0; j < 16; ++j) red[wave][m][lane_n * 16 + j] = part[m][j];
+      for (int j = 0; j < 16; ++j) part[m][j] = 0.f;
   }
-  __syncthreads();
-  // ... then over the 4 waves, fixed order.
-  for (int e = t; e < MT * kTileN; e += kThreads) {
-    const int m = e / kTileN, cc = e % kTileN;
-    const int col = tile * kTileN + cc;
-    if (m >= m_rows || col >= n) continue;
-    const float v = red[0][m][cc] + red[1][m][cc] + red[2][m][cc] + red[3][m][cc];
-    if (splits == 1) {
-      float o = v;
-      if (bias) o += h2f<T>(bias[col]);
-      c[static_cast<int64_t>(m) * n + col] = elem<T>::from_f32(o);
-    } else {
-      ws[(static_cast<int64_t>(split) * m_rows + m) * n + col] = v;
+
+  // Row-lane reduction through LDS (fixed order), one activation row at a time.
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    if (m > 0) __syncthreads();  // previous row's reads are done
+#pragma unroll
+    for (int j = 0; j < 16; j += 4)
+      *reinterpret_cast<float4*>(&red[rblk][lane_n * 16 + j]) =
+          make_float4(part[m][j], part[m][j + 1], part[m][j + 2], part[m][j + 3]);
+    __syncthreads();
+    if (t < kTileN && m < m_rows) {
+      const int col = tile * kTileN + t;
+      float v = 0.f;
+#pragma unroll 8
+      for (int r = 0; r < kRowsPar; ++r) v += red[r][t];
+      if (col < n) {
+        if (splits == 1) {
+          if (bias) v += h2f<T>(bias[col]);
+          c[static_cast<int64_t>(m) * n + col] = elem<T>::from_f32(v);
+        } else {
+          ws[(static_cast<int64_t>(split) * m_rows + m) * n + col] = v;
+        }
+      }
     }
   }
-  if (splits == 1) return;
+}
 
-  // Publish this split; the last arrival reduces all splits in order.
-  __threadfence();
-  __syncthreads();
-  if (t == 0) {
-    const unsigned prev = atomicAdd(&counters[tile], 1u);
-    last_flag = (prev == static_cast<unsigned>(splits - 1));
+// Sum of the split planes ws[split][row][col] in split order, + bias, -> C.
+template <typename T>
+__global__ void __launch_bounds__(kThreads)
+reduce_kernel(uint16_t* __restrict__ c, const float* __restrict__ ws,
+              const uint16_t* __restrict__ bias, int64_t rows, int64_t n, int splits) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (idx >= rows * n) return;
+  const int64_t plane = rows * n;
+  float p[8];
+  float o = 0.f;
+  int sp = 0;
+  for (; sp + 8 <= splits; sp += 8) {  // 8 independent loads in flight
+#pragma unroll
+    for (int i = 0; i < 8; ++i) p[i] = ws[(sp + i) * plane + idx];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o += p[i];
   }
-  __syncthreads();
-  if (!last_flag) return;
-  __threadfence();
-  for (int e = t; e < MT * kTileN; e += kThreads) {
-    const int m = e / kTileN, cc = e % kTileN;
-    const int col = tile * kTileN + cc;
-    if (m >= m_rows || col >= n) continue;
-    float o = 0.f;
-    for (int sp = 0; sp < splits; ++sp)
-      o += ws[(static_cast<int64_t>(sp) * m_rows + m) * n + col];
-    if (bias) o += h2f<T>(bias[col]);
-    c[static_cast<int64_t>(m) * n + col] = elem<T>::from_f32(o);
-  }
-  if (t == 0) counters[tile] = 0u;  // ready for the next call on this stream
+  for (; sp < splits; ++sp) o += ws[sp * plane + idx];
+  if (bias) o += h2f<T>(bias[idx % n]);
+  c[idx] = elem<T>::from_f32(o);
 }
 
 // Any-shape fallback: one thread per output element, full K loop, the
@@ -234,7 +251,6 @@ simple_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
   c[m * n + col] = elem<T>::from_f32(acc);
 }
 
-
 // ---------------------------------------------------------------------------
 // Batched MFMA path.
 // ---------------------------------------------------------------------------
@@ -244,11 +260,10 @@ mfma_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
             const uint8_t* __restrict__ b, const uint16_t* __restrict__ scales,
             const uint16_t* __restrict__ zeros, const uint16_t* __restrict__ bias,
             int64_t row0, int64_t row1, int64_t n, int64_t k, int gs, int splits,
-            int groups_per_split, float* __restrict__ ws, unsigned* __restrict__ counters) {
+            int groups_per_split, float* __restrict__ ws) {
   constexpr int kRows = 16 * MB;
   constexpr int kPlane = kRows * w4mma::kTileN;
   __shared__ float red[4 * kPlane];
-  __shared__ int last_flag;
   int tile, split;
   map_tile(blockIdx.x, gridDim.x, splits, &tile, &split);
   const int ng = static_cast<int>(k / gs);
@@ -260,51 +275,30 @@ mfma_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
   p.g_end = min(p.g_begin + groups_per_split, ng);
   w4mma::tile_partial<T, MB>(p, row0, red);
   const float* res = red + 3 * kPlane;
-  const int t = threadIdx.x;
   const int64_t rows = row1 - row0;
-  if (splits == 1) {
-    for (int e = t; e < kPlane; e += w4mma::kThreads) {
-      const int64_t r = e / w4mma::kTileN, col = p.n0 + e % w4mma::kTileN;
-      if (r >= rows || col >= n) continue;
+  for (int e = threadIdx.x; e < kPlane; e += w4mma::kThreads) {
+    const int64_t r = e / w4mma::kTileN, col = p.n0 + e % w4mma::kTileN;
+    if (r >= rows || col >= n) continue;
+    if (splits == 1) {
       float o = res[e];
       if (bias) o += h2f<T>(bias[col]);
       c[(row0 + r) * n + col] = elem<T>::from_f32(o);
+    } else {
+      ws[(static_cast<int64_t>(split) * rows + r) * n + col] = res[e];
     }
-    return;
   }
-  for (int e = t; e < kPlane; e += w4mma::kThreads) {
-    const int64_t r = e / w4mma::kTileN, col = p.n0 + e % w4mma::kTileN;
-    if (r >= rows || col >= n) continue;
-    ws[(static_cast<int64_t>(split) * rows + r) * n + col] = res[e];
-  }
-  __threadfence();
-  __syncthreads();
-  if (t == 0) {
-    const unsigned prev = atomicAdd(&counters[tile], 1u);
-    last_flag = (prev == static_cast<unsigned>(splits - 1));
-  }
-  __syncthreads();
-  if (!last_flag) return;
-  __threadfence();
-  for (int e = t; e < kPlane; e += w4mma::kThreads) {
-    const int64_t r = e / w4mma::kTileN, col = p.n0 + e % w4mma::kTileN;
-    if (r >= rows || col >= n) continue;
-    float o = 0.f;
-    for (int sp = 0; sp < splits; ++sp) o += ws[(static_cast<int64_t>(sp) * rows + r) * n + col];
-    if (bias) o += h2f<T>(bias[col]);
-    c[(row0 + r) * n + col] = elem<T>::from_f32(o);
-  }
-  if (t == 0) counters[tile] = 0u;
 }
 
-template <typename T, int MB>
-void launch_mfma(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_t* s,
-                 const uint16_t* z, const uint16_t* bias, int64_t r0, int64_t r1, int64_t n,
-                 int64_t k, int gs, int tiles, int splits, int gps, const Scratch& sc,
-                 hipStream_t st) {
-  hipLaunchKernelGGL((mfma_kernel<T, MB>), dim3(tiles * splits), dim3(w4mma::kThreads), 0, st,
-                     c, a, b, s, z, bias, r0, r1, n, k, gs, splits, gps, sc.partial,
-                     sc.counters);
+inline bool aligned(const void* p, uintptr_t q) {
+  return p == nullptr || (reinterpret_cast<uintptr_t>(p) % q) == 0;
+}
+
+template <typename T>
+void launch_reduce(uint16_t* c, const float* ws, const uint16_t* bias, int64_t rows, int64_t n,
+                   int splits, hipStream_t st) {
+  const int64_t total = rows * n;
+  hipLaunchKernelGGL((reduce_kernel<T>), dim3(static_cast<unsigned>((total + kThreads - 1) / kThreads)),
+                     dim3(kThreads), 0, st, c, ws, bias, rows, n, splits);
 }
 
 template <typename T>
@@ -321,39 +315,33 @@ ks_status_t run_mfma(uint16_t* c, const uint16_t* a, const uint8_t* b, const uin
   const int mb_rows = m >= 64 ? 64 : (m > 16 ? 32 : 16);
   Scratch sc;
   if (splits > 1) {
-    ks_status_t r = get_scratch(st, static_cast<size_t>(splits) * mb_rows * n,
-                                static_cast<size_t>(tiles), &sc, "ks_gemm_w4a16");
+    ks_status_t r = get_scratch(st, static_cast<size_t>(splits) * mb_rows * n, 0, &sc,
+                                "ks_gemm_w4a16");
     if (r != KS_SUCCESS) return r;
   }
   for (int64_t r0 = 0; r0 < m; r0 += mb_rows) {
     const int64_t r1 = std::min(m, r0 + mb_rows);
-    if (mb_rows == 64) launch_mfma<T, 4>(c, a, b, s, z, bias, r0, r1, n, k, gs, tiles, splits, gps, sc, st);
-    else if (mb_rows == 32) launch_mfma<T, 2>(c, a, b, s, z, bias, r0, r1, n, k, gs, tiles, splits, gps, sc, st);
-    else launch_mfma<T, 1>(c, a, b, s, z, bias, r0, r1, n, k, gs, tiles, splits, gps, sc, st);
+    const dim3 grid(tiles * splits), block(w4mma::kThreads);
+    if (mb_rows == 64)
+      hipLaunchKernelGGL((mfma_kernel<T, 4>), grid, block, 0, st, c, a, b, s, z, bias, r0, r1, n, k, gs, splits, gps, sc.partial);
+    else if (mb_rows == 32)
+      hipLaunchKernelGGL((mfma_kernel<T, 2>), grid, block, 0, st, c, a, b, s, z, bias, r0, r1, n, k, gs, splits, gps, sc.partial);
+    else
+      hipLaunchKernelGGL((mfma_kernel<T, 1>), grid, block, 0, st, c, a, b, s, z, bias, r0, r1, n, k, gs, splits, gps, sc.partial);
+    if (splits > 1) launch_reduce<T>(c + r0 * n, sc.partial, bias, r1 - r0, n, splits, st);
   }
   return KS_SUCCESS;
 }
 
-inline bool aligned(const void* p, uintptr_t q) {
-  return p == nullptr || (reinterpret_cast<uintptr_t>(p) % q) == 0;
-}
-
-template <typename T, int MT, int RPT>
+template <typename T, int RPT>
 void launch_gemv(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_t* s,
                  const uint16_t* z, const uint16_t* bias, int m, int n, int k, int gs,
-                 int tiles, int splits, const Scratch& sc, hipStream_t st) {
-  hipLaunchKernelGGL((gemv_kernel<T, MT, RPT>), dim3(tiles * splits), dim3(kThreads), 0, st, c,
-                     a, b, s, z, bias, m, n, k, gs, splits, sc.partial, sc.counters);
-}
-
-template <typename T, int RPT>
-void launch_gemv_m(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_t* s,
-                   const uint16_t* z, const uint16_t* bias, int m, int n, int k, int gs,
-                   int tiles, int splits, const Scratch& sc, hipStream_t st) {
-  if (m <= 1) launch_gemv<T, 1, RPT>(c, a, b, s, z, bias, m, n, k, gs, tiles, splits, sc, st);
-  else if (m <= 2) launch_gemv<T, 2, RPT>(c, a, b, s, z, bias, m, n, k, gs, tiles, splits, sc, st);
-  else if (m <= 4) launch_gemv<T, 4, RPT>(c, a, b, s, z, bias, m, n, k, gs, tiles, splits, sc, st);
-  else launch_gemv<T, 8, RPT>(c, a, b, s, z, bias, m, n, k, gs, tiles, splits, sc, st);
+                 int tiles, int splits, float* ws, hipStream_t st) {
+  const dim3 grid(tiles * splits), block(kThreads);
+  if (m <= 1) hipLaunchKernelGGL((gemv_kernel<T, 1, RPT>), grid, block, 0, st, c, a, b, s, z, bias, m, n, k, gs, splits, ws);
+  else if (m <= 2) hipLaunchKernelGGL((gemv_kernel<T, 2, RPT>), grid, block, 0, st, c, a, b, s, z, bias, m, n, k, gs, splits, ws);
+  else if (m <= 4) hipLaunchKernelGGL((gemv_kernel<T, 4, RPT>), grid, block, 0, st, c, a, b, s, z, bias, m, n, k, gs, splits, ws);
+  else hipLaunchKernelGGL((gemv_kernel<T, 8, RPT>), grid, block, 0, st, c, a, b, s, z, bias, m, n, k, gs, splits, ws);
 }
 
 template <typename T>
@@ -380,17 +368,17 @@ ks_status_t run(void* c_, const void* a_, const void* b_, const void* s_, const 
   }
   const int tiles = static_cast<int>((n + kTileN - 1) / kTileN);
   const int64_t kp = k / 2;
-  // Eight packed rows per thread unless that leaves fewer than 512 workgroups.
+  // Eight packed rows per thread unless that leaves fewer than 256 workgroups.
   int rpt = 8;
   int splits = static_cast<int>((kp + kRowsPar * rpt - 1) / (kRowsPar * rpt));
-  if (static_cast<int64_t>(tiles) * splits < 512) {
+  if (static_cast<int64_t>(tiles) * splits < 256) {
     rpt = 4;
     splits = static_cast<int>((kp + kRowsPar * rpt - 1) / (kRowsPar * rpt));
   }
   Scratch sc;
   if (splits > 1) {
-    ks_status_t r = get_scratch(st, static_cast<size_t>(splits) * kMaxGemvM * n,
-                                static_cast<size_t>(tiles), &sc, "ks_gemm_w4a16");
+    ks_status_t r = get_scratch(st, static_cast<size_t>(splits) * kMaxGemvM * n, 0, &sc,
+                                "ks_gemm_w4a16");
     if (r != KS_SUCCESS) return r;
   }
   for (int64_t m0 = 0; m0 < m; m0 += kMaxGemvM) {
@@ -398,8 +386,9 @@ ks_status_t run(void* c_, const void* a_, const void* b_, const void* s_, const 
     uint16_t* cc = c + m0 * n;
     const uint16_t* aa = a + m0 * k;
     const int ki = static_cast<int>(k), ni = static_cast<int>(n);
-    if (rpt == 8) launch_gemv_m<T, 8>(cc, aa, b, s, z, bias, mm, ni, ki, gs, tiles, splits, sc, st);
-    else launch_gemv_m<T, 4>(cc, aa, b, s, z, bias, mm, ni, ki, gs, tiles, splits, sc, st);
+    if (rpt == 8) launch_gemv<T, 8>(cc, aa, b, s, z, bias, mm, ni, ki, gs, tiles, splits, sc.partial, st);
+    else launch_gemv<T, 4>(cc, aa, b, s, z, bias, mm, ni, ki, gs, tiles, splits, sc.partial, st);
+    if (splits > 1) launch_reduce<T>(cc, sc.partial, bias, mm, n, splits, st);
   }
   return KS_SUCCESS;
 }
