@@ -285,7 +285,7 @@ def main():
         sec = {}
         steps = max(64, args.steps // 8)
         fn, per, nb, fl = wl_fp8_gemm(torch, ks, H)
-        ms2, c2 = T.run(fn, per, max(32, steps // 8), 8)
+        ms2, c2 = T.run(fn, per, max(32, steps // 8), 8, min_per_graph=8)
         sec["fp8_blockwise_gemm_M2048_N7168_K7168"] = line("fp8 gemm", ms2, c2, nb, fl, "mfma", "fp8")
         fn, per, nb, fl = wl_quant_group(torch, ks, H, 16)
         ms2, c2 = T.run(fn, per, steps, 32)
@@ -299,7 +299,7 @@ def main():
             d["bound"] = "hbm" if nb / (HBM_PEAK_GBS * 1e9) >= fl / (PEAK_TFLOPS["bf16"] * 1e12) else "mfma-bf16"
             sec[f"w4a16_M{mm}_K4096_N14336_cold"] = d
         fn, per, nb, fl = wl_w8a8(torch, ks, H)
-        ms2, c2 = T.run(fn, per, max(32, steps // 8), 8)
+        ms2, c2 = T.run(fn, per, max(32, steps // 8), 8, min_per_graph=8)
         sec["w8a8_M4096_N4096_K4096"] = line("w8a8", ms2, c2, nb, fl, "mfma", "int8")
         for K_, N_, nm in ((2048, 1536, "gate_up"), (768, 2048, "down")):
             fn, per, nb, fl = wl_moe(torch, ks, H, K_, N_, 4)

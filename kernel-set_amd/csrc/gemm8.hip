@@ -277,6 +277,209 @@ gemm8_kernel(Args p) {
     }
 }
 
+
+// ===========================================================================
+// Fast path: 256x256 workgroup tile, 8 waves (2 x 4) of 128x64, K step 128,
+// LDS double buffer, one barrier per K step, no VGPR staging:
+//  * A [256 rows][128 B] and B [128 k][256 n] tiles are fetched with
+//    global_load_lds_dwordx4 straight into LDS; every wave instruction fills a
+//    contiguous 1 KB and each lane picks which 16-byte chunk lands in its slot,
+//    which stores both tiles with their chunks XOR-swizzled by (row & 7).
+//  * A fragments: two ds_read_b128 per 16x(32 k) lane slice.
+//  * B fragments are read already transposed with ds_read_b64_tr_b8: in each
+//    16-lane group, lanes (2j, 2j+1) address the two 8-byte halves of k-row j
+//    of a 16-column block and lane i receives column i of those 8 rows, i.e.
+//    8 consecutive k of one column, the MFMA operand order. With the swizzle
+//    the 16 reads of a group touch 16 distinct 8-byte bank slots.
+//  * fp8 (block_k == 128): each 16x16x128 MFMA is one whole scale block, so the
+//    partial is promoted at once: O = fma(P, a_s * b_s, O). The two scale
+//    vectors of a step are also fetched straight into LDS.
+// ===========================================================================
+constexpr int kFThreads = 512;
+constexpr int kFBM = 256, kFBN = 256;
+constexpr int kFARow = 128;  // bytes per A row in LDS
+constexpr int kFBRow = 256;  // bytes per B k-row in LDS
+
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
+
+template <int KIND, typename Out>
+__global__ void __launch_bounds__(kFThreads)
+gemm8_fast_kernel(Args p) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  uint8_t* sA = smem;                                   // [2][256][128]
+  uint8_t* sB = smem + 2 * kFBM * kFARow;               // [2][128][256]
+  float* sAs = reinterpret_cast<float*>(sB + 2 * kBK * kFBRow);  // [2][256]
+  float* sBs = sAs + 2 * kFBM;                                   // [2][256]
+
+  const int tiles_m = static_cast<int>((p.m + kFBM - 1) / kFBM);
+  const int tiles_n = static_cast<int>(p.n / kFBN);
+  int tm, tn;
+  tile_coords(blockIdx.x, tiles_m, tiles_n, &tm, &tn);
+  const int64_t m0 = static_cast<int64_t>(tm) * kFBM;
+  const int64_t n0 = static_cast<int64_t>(tn) * kFBN;
+
+  const int t = threadIdx.x;
+  const int lane = t % kWave;
+  const int wave = t / kWave;
+  const int wm = (wave / 4) * 128;
+  const int wn = (wave % 4) * 64;
+  const int li = lane % 16, lk = lane / 16;
+  constexpr bool kFp8 = (KIND == FP8_E4M3 || KIND == FP8_E5M2);
+
+  // ---- per-lane global offsets of the direct-to-LDS loads (32-bit, checked
+  // on the host). A: wave instruction i fills rows 8*(4*wave+i)..+7.
+  uint32_t a_off[4], b_off[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 8 * (4 * wave + i) + lane / 8;
+    const int64_t gm = min<int64_t>(m0 + row, p.m - 1);  // rows past M are never stored
+    a_off[i] = static_cast<uint32_t>(gm * p.k + 16 * ((lane % 8) ^ (row & 7)));
+    const int krow = 4 * (4 * wave + i) + lane / 16;       // B: 4 k-rows per instruction
+    b_off[i] = static_cast<uint32_t>(krow * p.n + n0 + 16 * ((lane % 16) ^ (krow & 7)));
+  }
+  const uint32_t n32 = static_cast<uint32_t>(p.n);
+  // scales: waves 0-3 fetch a_scale of rows 64*wave+lane, waves 4-7 b_scale
+  const int s_idx = 64 * (wave % 4) + lane;
+  const int64_t s_m = min<int64_t>(m0 + s_idx, p.m - 1);
+  const int64_t s_n = n0 + s_idx;
+
+  auto issue_loads = [&](int step, int buf) {
+    const uint32_t k0 = static_cast<uint32_t>(step * kBK);
+    uint8_t* a_dst = sA + buf * kFBM * kFARow + (4 * wave) * 8 * kFARow;
+    uint8_t* b_dst = sB + buf * kBK * kFBRow + (4 * wave) * 4 * kFBRow;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      __builtin_amdgcn_global_load_lds(p.a + (a_off[i] + k0), a_dst + i * 8 * kFARow, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(p.b + (b_off[i] + k0 * n32), b_dst + i * 4 * kFBRow, 16, 0, 0);
+    }
+    if constexpr (kFp8) {
+      const int64_t kb = step;  // block_k == 128
+      if (wave < 4)
+        __builtin_amdgcn_global_load_lds(p.a_scale + (s_m * p.nkb + kb),
+                                         sAs + buf * kFBM + 64 * wave, 4, 0, 0);
+      else
+        __builtin_amdgcn_global_load_lds(p.b_scale + (kb * p.nnb + s_n / p.block_n),
+                                         sBs + buf * kFBN + 64 * (wave - 4), 4, 0, 0);
+    }
+  };
+
+  f32x4 acc_o[8][4];
+  i32x4 acc_i[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      acc_o[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      acc_i[i][j] = i32x4{0, 0, 0, 0};
+    }
+
+  // B transposed-read addressing: lane (2*jj + h) of its 16-lane group reads
+  // k-row (kbase + jj), bytes 8h..8h+7 of the 16-column block.
+  const int tr_jj = li >> 1, tr_h = li & 1;
+
+  const int steps = static_cast<int>(p.k / kBK);
+  issue_loads(0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int s = 0; s < steps; ++s) {
+    const int cur = s & 1;
+    if (s + 1 < steps) issue_loads(s + 1, cur ^ 1);
+    const uint8_t* a_src = sA + cur * kFBM * kFARow;
+    const uint8_t* b_src = sB + cur * kBK * kFBRow;
+
+    // B fragment of n-block j: k rows kb0 + 0..KLEN-1 of columns wn+16j..+15
+    auto b_tr8 = [&](int j, int krow) -> i32x2 {
+      const int row = krow + tr_jj;
+      const int chunk = ((wn + 16 * j) >> 4) ^ (row & 7);
+      const uint8_t* addr = b_src + row * kFBRow + chunk * 16 + 8 * tr_h;
+      return __builtin_amdgcn_ds_read_tr8_b64_v2i32(reinterpret_cast<lds_i32x2*>(
+          reinterpret_cast<uintptr_t>(addr)));
+    };
+
+    if constexpr (kFp8) {
+      i32x8 fb[4];
+      float bs[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const i32x2 q0 = b_tr8(j, 32 * lk + 0), q1 = b_tr8(j, 32 * lk + 8);
+        const i32x2 q2 = b_tr8(j, 32 * lk + 16), q3 = b_tr8(j, 32 * lk + 24);
+        fb[j] = i32x8{q0[0], q0[1], q1[0], q1[1], q2[0], q2[1], q3[0], q3[1]};
+        bs[j] = sBs[cur * kFBN + wn + 16 * j + li];
+      }
+      constexpr int fmt = (KIND == FP8_E5M2) ? 1 : 0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int row = wm + 16 * i + li;
+        const uint8_t* pa = a_src + row * kFARow;
+        const uint4 x0 = *reinterpret_cast<const uint4*>(pa + ((2 * lk) ^ (row & 7)) * 16);
+        const uint4 x1 = *reinterpret_cast<const uint4*>(pa + ((2 * lk + 1) ^ (row & 7)) * 16);
+        const i32x8 fa = i32x8{(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w,
+                               (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+        const f32x4 as4 = *reinterpret_cast<const f32x4*>(&sAs[cur * kFBM + wm + 16 * i + 4 * lk]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const f32x4 part = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+              fa, fb[j], f32x4{0.f, 0.f, 0.f, 0.f}, fmt, fmt, 0, 127, 0, 127);
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            acc_o[i][j][r] = fmaf(part[r], as4[r] * bs[j], acc_o[i][j][r]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        i32x4 fb[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const i32x2 q0 = b_tr8(j, 64 * h + 16 * lk), q1 = b_tr8(j, 64 * h + 16 * lk + 8);
+          fb[j] = i32x4{q0[0], q0[1], q1[0], q1[1]};
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int row = wm + 16 * i + li;
+          const uint4 x = *reinterpret_cast<const uint4*>(a_src + row * kFARow +
+                                                          ((4 * h + lk) ^ (row & 7)) * 16);
+          const i32x4 fa = i32x4{(int)x.x, (int)x.y, (int)x.z, (int)x.w};
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc_i[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa, fb[j], acc_i[i][j], 0, 0, 0);
+        }
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's loads for step s+1 have landed
+    __syncthreads();
+  }
+
+  // ---- epilogue: lane holds rows wm+16i+4lk+r, column wn+16j+li ----
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t gn = n0 + wn + 16 * j + li;
+    float bsc = 0.f;
+    if constexpr (KIND == INT8) bsc = p.b_per_channel ? p.b_scale[gn] : p.b_scale[0];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t gm = m0 + wm + 16 * i + 4 * lk + r;
+        if (gm >= p.m) continue;
+        if constexpr (kFp8) {
+          store_out<Out>(static_cast<typename Out::storage*>(p.out) + gm * p.n + gn, acc_o[i][j][r]);
+        } else if constexpr (KIND == INT8_RAW) {
+          static_cast<int32_t*>(p.out)[gm * p.n + gn] = acc_i[i][j][r];
+        } else {
+          const float as = p.a_per_token ? p.a_scale[gm] : p.a_scale[0];
+          float v = __fmul_rn(__fmul_rn(static_cast<float>(acc_i[i][j][r]), as), bsc);
+          if (p.bias)
+            v = __fadd_rn(v, elem<Out>::load(static_cast<const typename Out::storage*>(p.bias), gn));
+          store_out<Out>(static_cast<typename Out::storage*>(p.out) + gm * p.n + gn, v);
+        }
+      }
+  }
+}
+
+constexpr size_t kFastLds = 2 * kFBM * kFARow + 2 * kBK * kFBRow + 2 * (kFBM + kFBN) * sizeof(float);
+
 // Any-shape fp8 blockwise fallback (one thread per output, reference order).
 template <typename Dec, typename Out>
 __global__ void __launch_bounds__(kThreads)
@@ -332,6 +535,27 @@ void launch_tiled(const Args& p, hipStream_t s) {
                      dim3(kThreads), 0, s, p);
 }
 
+// The fast kernel covers shapes without K/N tails whose operands fit 32-bit
+// byte offsets; everything else takes the general tiled kernel.
+inline bool fast_ok(const Args& p) {
+  return p.k % kBK == 0 && p.n % kFBN == 0 && p.m * p.k < (int64_t{1} << 31) &&
+         p.k * p.n < (int64_t{1} << 31) && (reinterpret_cast<uintptr_t>(p.a) & 15u) == 0 &&
+         (reinterpret_cast<uintptr_t>(p.b) & 15u) == 0;
+}
+
+template <int KIND, typename Out>
+void launch_fast(const Args& p, hipStream_t s) {
+  static bool configured = false;  // opt in to the LDS size once per process
+  if (!configured) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm8_fast_kernel<KIND, Out>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kFastLds));
+    configured = true;
+  }
+  const int64_t tiles = ((p.m + kFBM - 1) / kFBM) * ((p.n + kFBN - 1) / kFBN);
+  hipLaunchKernelGGL((gemm8_fast_kernel<KIND, Out>), dim3(static_cast<unsigned>(tiles)),
+                     dim3(kFThreads), kFastLds, s, p);
+}
+
 inline unsigned simple_grid(const Args& p) {
   return static_cast<unsigned>((p.m * p.n + kThreads - 1) / kThreads);
 }
@@ -339,18 +563,22 @@ inline unsigned simple_grid(const Args& p) {
 template <typename Out>
 void run_fp8(const Args& p, ks_dtype_t fp8, hipStream_t s) {
   const bool tiled = tiled_ok(p) && p.block_k % kBK == 0;
+  const bool fast = tiled && p.block_k == kBK && fast_ok(p);
   if (fp8 == KS_DTYPE_F8E4M3) {
-    if (tiled) launch_tiled<FP8_E4M3, Out>(p, s);
+    if (fast) launch_fast<FP8_E4M3, Out>(p, s);
+    else if (tiled) launch_tiled<FP8_E4M3, Out>(p, s);
     else hipLaunchKernelGGL((fp8_blockwise_simple_kernel<e4m3_t, Out>), dim3(simple_grid(p)), dim3(kThreads), 0, s, p);
   } else {
-    if (tiled) launch_tiled<FP8_E5M2, Out>(p, s);
+    if (fast) launch_fast<FP8_E5M2, Out>(p, s);
+    else if (tiled) launch_tiled<FP8_E5M2, Out>(p, s);
     else hipLaunchKernelGGL((fp8_blockwise_simple_kernel<e5m2_t, Out>), dim3(simple_grid(p)), dim3(kThreads), 0, s, p);
   }
 }
 
 template <int KIND, typename Out>
 void run_w8a8(const Args& p, hipStream_t s) {
-  if (tiled_ok(p)) launch_tiled<KIND, Out>(p, s);
+  if (tiled_ok(p) && fast_ok(p)) launch_fast<KIND, Out>(p, s);
+  else if (tiled_ok(p)) launch_tiled<KIND, Out>(p, s);
   else hipLaunchKernelGGL((w8a8_simple_kernel<KIND, Out>), dim3(simple_grid(p)), dim3(kThreads), 0, s, p);
 }
 
