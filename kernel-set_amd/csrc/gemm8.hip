@@ -303,7 +303,7 @@ constexpr int kFBRow = 256;  // bytes per B k-row in LDS
 typedef int i32x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
 
-template <int KIND, typename Out>
+template <int KIND, typename Out, bool UNIFORM_BS>
 __global__ void __launch_bounds__(kFThreads)
 gemm8_fast_kernel(Args p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -341,8 +341,13 @@ gemm8_fast_kernel(Args p) {
   const uint32_t n32 = static_cast<uint32_t>(p.n);
   // scales: waves 0-3 fetch a_scale of rows 64*wave+lane, waves 4-7 b_scale
   const int s_idx = 64 * (wave % 4) + lane;
-  const int64_t s_m = min<int64_t>(m0 + s_idx, p.m - 1);
-  const int64_t s_n = n0 + s_idx;
+  const float* s_src = nullptr;
+  int64_t s_step = 0;  // per K block
+  if constexpr (kFp8) {
+    s_src = (wave < 4) ? p.a_scale + min<int64_t>(m0 + s_idx, p.m - 1) * p.nkb
+                       : p.b_scale + (n0 + s_idx) / p.block_n;
+    s_step = (wave < 4) ? 1 : p.nnb;
+  }
 
   auto issue_loads = [&](int step, int buf) {
     const uint32_t k0 = static_cast<uint32_t>(step * kBK);
@@ -353,14 +358,9 @@ gemm8_fast_kernel(Args p) {
       __builtin_amdgcn_global_load_lds(p.a + (a_off[i] + k0), a_dst + i * 8 * kFARow, 16, 0, 0);
       __builtin_amdgcn_global_load_lds(p.b + (b_off[i] + k0 * n32), b_dst + i * 4 * kFBRow, 16, 0, 0);
     }
-    if constexpr (kFp8) {
-      const int64_t kb = step;  // block_k == 128
-      if (wave < 4)
-        __builtin_amdgcn_global_load_lds(p.a_scale + (s_m * p.nkb + kb),
-                                         sAs + buf * kFBM + 64 * wave, 4, 0, 0);
-      else
-        __builtin_amdgcn_global_load_lds(p.b_scale + (kb * p.nnb + s_n / p.block_n),
-                                         sBs + buf * kFBN + 64 * (wave - 4), 4, 0, 0);
+    if constexpr (kFp8) {  // block_k == 128: K step `step` is scale block `step`
+      float* s_dst = (wave < 4) ? sAs + buf * kFBM + 64 * wave : sBs + buf * kFBN + 64 * (wave - 4);
+      __builtin_amdgcn_global_load_lds(s_src + step * s_step, s_dst, 4, 0, 0);
     }
   };
 
@@ -408,22 +408,43 @@ gemm8_fast_kernel(Args p) {
         bs[j] = sBs[cur * kFBN + wn + 16 * j + li];
       }
       constexpr int fmt = (KIND == FP8_E5M2) ? 1 : 0;
+      // The MFMAs of row block i are issued before the promotion of row block
+      // i-1, so promotions never wait on a just-issued MFMA.
+      f32x4 part[2][4];
+      f32x4 scl[2];
+      // A fragment: the chunk swizzle (row & 7) equals (li & 7) for every row block.
+      const uint8_t* pa0 = a_src + (wm + li) * kFARow;
+      const int ca0 = ((2 * lk) ^ (li & 7)) * 16, ca1 = ((2 * lk + 1) ^ (li & 7)) * 16;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int row = wm + 16 * i + li;
-        const uint8_t* pa = a_src + row * kFARow;
-        const uint4 x0 = *reinterpret_cast<const uint4*>(pa + ((2 * lk) ^ (row & 7)) * 16);
-        const uint4 x1 = *reinterpret_cast<const uint4*>(pa + ((2 * lk + 1) ^ (row & 7)) * 16);
-        const i32x8 fa = i32x8{(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w,
-                               (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
-        const f32x4 as4 = *reinterpret_cast<const f32x4*>(&sAs[cur * kFBM + wm + 16 * i + 4 * lk]);
+      for (int i = 0; i <= 8; ++i) {
+        if (i < 8) {
+          const uint8_t* pa = pa0 + i * 16 * kFARow;
+          const uint4 x0 = *reinterpret_cast<const uint4*>(pa + ca0);
+          const uint4 x1 = *reinterpret_cast<const uint4*>(pa + ca1);
+          const i32x8 fa = i32x8{(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w,
+                                 (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+          scl[i & 1] = *reinterpret_cast<const f32x4*>(&sAs[cur * kFBM + wm + 16 * i + 4 * lk]);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const f32x4 part = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-              fa, fb[j], f32x4{0.f, 0.f, 0.f, 0.f}, fmt, fmt, 0, 127, 0, 127);
+          for (int j = 0; j < 4; ++j)
+            part[i & 1][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                fa, fb[j], f32x4{0.f, 0.f, 0.f, 0.f}, fmt, fmt, 0, 127, 0, 127);
+        }
+        if (i > 0) {
+          const int ip = i - 1, sp = ip & 1;
+          if constexpr (UNIFORM_BS) {  // block_n % 64 == 0: one b_scale per wave
+            const f32x4 sc = scl[sp] * bs[0];
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            acc_o[i][j][r] = fmaf(part[r], as4[r] * bs[j], acc_o[i][j][r]);
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                acc_o[ip][j][r] = fmaf(part[sp][j][r], sc[r], acc_o[ip][j][r]);
+          } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                acc_o[ip][j][r] = fmaf(part[sp][j][r], scl[sp][r] * bs[j], acc_o[ip][j][r]);
+          }
         }
       }
     } else {
@@ -543,17 +564,27 @@ inline bool fast_ok(const Args& p) {
          (reinterpret_cast<uintptr_t>(p.b) & 15u) == 0;
 }
 
-template <int KIND, typename Out>
-void launch_fast(const Args& p, hipStream_t s) {
+template <int KIND, typename Out, bool UBS>
+void launch_fast_impl(const Args& p, hipStream_t s) {
   static bool configured = false;  // opt in to the LDS size once per process
   if (!configured) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm8_fast_kernel<KIND, Out>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm8_fast_kernel<KIND, Out, UBS>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kFastLds));
     configured = true;
   }
   const int64_t tiles = ((p.m + kFBM - 1) / kFBM) * ((p.n + kFBN - 1) / kFBN);
-  hipLaunchKernelGGL((gemm8_fast_kernel<KIND, Out>), dim3(static_cast<unsigned>(tiles)),
+  hipLaunchKernelGGL((gemm8_fast_kernel<KIND, Out, UBS>), dim3(static_cast<unsigned>(tiles)),
                      dim3(kFThreads), kFastLds, s, p);
+}
+
+// A wave's 64 columns share one b_scale entry when block_n is a multiple of 64
+// (n0 and the wave offsets are multiples of 64).
+template <int KIND, typename Out>
+void launch_fast(const Args& p, hipStream_t s) {
+  if ((KIND == FP8_E4M3 || KIND == FP8_E5M2) && p.block_n % 64 == 0)
+    launch_fast_impl<KIND, Out, true>(p, s);
+  else
+    launch_fast_impl<KIND, Out, false>(p, s);
 }
 
 inline unsigned simple_grid(const Args& p) {
