@@ -48,9 +48,10 @@ def log(*a):
 class Timer:
     """Graph-captured replay timing on a dedicated stream."""
 
-    def __init__(self, torch):
+    def __init__(self, torch, graph=True):
         self.torch = torch
         self.stream = torch.cuda.Stream()
+        self.graph = graph
 
     def run(self, fn, rotate, steps, warmup, min_per_graph=64):
         """fn(i) issues call i on buffer set i (i < rotate). Each graph holds at
@@ -64,6 +65,8 @@ class Timer:
             for i in range(per_graph):  # eager warm-up: allocates library scratch
                 fn(i)
         torch.cuda.synchronize()
+        if not self.graph:
+            return self._run_eager(fn, steps, warmup)
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=self.stream):
             for i in range(per_graph):
@@ -84,6 +87,55 @@ class Timer:
         ms = start.elapsed_time(end) / calls
         del g
         return ms, calls
+
+    def _run_eager(self, fn, steps, warmup):
+        """Plain launches, each call bracketed by its own event pair on the
+        launch stream (profiler-friendly: no graph). Returns the mean
+        event-measured duration of one call."""
+        torch = self.torch
+        with torch.cuda.stream(self.stream):
+            for i in range(warmup):
+                fn(i)
+            torch.cuda.synchronize()
+            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                  for _ in range(steps)]
+            # A bounded spin kernel holds the stream while the host enqueues
+            # every call, so the event pairs time GPU execution, not host gaps.
+            torch.cuda._sleep(self._sleep_cycles(steps * 300e-6))
+            for i, (a, b) in enumerate(ev):
+                a.record()
+                fn(i)
+                b.record()
+        torch.cuda.synchronize()
+        return sum(a.elapsed_time(b) for a, b in ev) / steps, steps
+
+    def _sleep_cycles(self, seconds):
+        torch = self.torch
+        if not hasattr(self, "_cyc_per_s"):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            with torch.cuda.stream(self.stream):
+                a.record()
+                torch.cuda._sleep(1 << 20)
+                b.record()
+            torch.cuda.synchronize()
+            self._cyc_per_s = (1 << 20) / max(a.elapsed_time(b) * 1e-3, 1e-6)
+        return int(min(seconds, 1.0) * self._cyc_per_s)
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "w4a16_gemv_M1_K4096_N4096_hbm_bytes.md")
+
+
+def measured_traffic():
+    """HBM bytes per headline call from the committed rocprofv3 PMC summary
+    (FETCH_SIZE and WRITE_SIZE per dispatch, scaled by a copy calibration)."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for ln in f:
+                if ln.startswith("traffic_bytes_per_call:"):
+                    return int(ln.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    return None
 
 
 def rot_copies(t, n):
@@ -231,6 +283,10 @@ def main():
     ap.add_argument("--rotate", type=int, default=64)
     ap.add_argument("--only", default="all", help="all | headline")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--no-graph", action="store_true",
+                    help="plain launches with per-call events (for rocprofv3 runs)")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="only run --steps device copies of this many MiB (PMC byte calibration)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -240,13 +296,22 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.calib_copy_mib:
+        nb = args.calib_copy_mib << 20
+        src = torch.empty(nb, dtype=torch.uint8, device="cuda").fill_(7)
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calib_copy_bytes": nb, "copies": args.steps}), flush=True)
+        return
     import kernel_set as ks
     from tests import helpers as H
 
     dev_name = torch.cuda.get_device_name(0)
     props = torch.cuda.get_device_properties(0)
     log(f"device: {dev_name} {getattr(props, 'gcnArchName', '')} CUs={props.multi_processor_count}")
-    T = Timer(torch)
+    T = Timer(torch, graph=not args.no_graph)
 
     # ---- headline: W4A16 GEMV, config 1 shape, cold weights ----------------
     m, k, n, gs = 1, 4096, 4096, 128
@@ -272,11 +337,14 @@ def main():
         "data": "synthetic (BASELINE config 1 distributions, seeded)",
         "config": {"workload": "w4a16_gemv", "M": m, "K": k, "N": n, "group_size": gs,
                    "zeros": "fixed 8.0", "weights": f"cold: {args.rotate} rotated copies",
-                   "timing": "HIP-graph replay, events on the replay stream",
+                   "timing": ("per-call events, plain launches" if args.no_graph else
+                              "HIP-graph replay, events on the replay stream"),
                    "device": dev_name},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "ks::w4a16::gemv_kernel", "bytes_per_launch": nbytes},
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(),
+                     "kernel": "ks_gemm_w4a16 call = ks::w4a16::gemv_kernel + reduce_kernel",
+                     "bytes_per_launch": nbytes},
         "warm_cache": {"us_per_call": round(ms_warm * 1e3, 3),
                        "GB/s": round(nbytes / (ms_warm * 1e-3) / 1e9, 2)},
     }

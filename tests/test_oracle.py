@@ -259,3 +259,55 @@ def test_w8a8_epilogue_order():
     out = O.w8a8_epilogue(acc, a_s, b_s)
     exp = ((acc.astype(np.float32) * a_s[0]).astype(np.float32) * b_s).astype(np.float32)
     assert np.array_equal(out, exp)
+
+
+def test_moe_topk_brute_force_and_ties():
+    """moe_gate.cu:88-105: k largest logits, the lowest expert id wins a tie."""
+    rng = np.random.default_rng(5)
+    lg = rng.standard_normal((40, 16)).astype(np.float32)
+    lg[0, [3, 7, 9]] = 5.0          # three-way tie at the top
+    lg[1, :] = 1.0                  # everything tied
+    ids = O.moe_topk_ids(lg, 4)
+    assert list(ids[0][:3]) == [3, 7, 9]
+    assert list(ids[1]) == [0, 1, 2, 3]
+    for t in range(lg.shape[0]):
+        best = sorted(range(16), key=lambda e: (-float(lg[t, e]), e))[:4]
+        assert list(ids[t]) == best
+
+
+def test_moe_group_rows_invariants():
+    rng = np.random.default_rng(6)
+    ids = O.moe_topk_ids(rng.standard_normal((33, 8)).astype(np.float32), 3)
+    for pad in (1, 4, 16):
+        src, offs = O.moe_group_rows(ids, 8, pad)
+        assert offs[0] == 0 and offs[-1] == len(src) and np.all(np.diff(offs) % pad == 0)
+        live = src[src >= 0]
+        assert sorted(live.tolist()) == list(range(ids.size))   # each (token, slot) once
+        flat = ids.reshape(-1)
+        for e in range(8):
+            blk = src[offs[e]:offs[e + 1]]
+            assert np.all(flat[blk[blk >= 0]] == e)
+            assert np.all(np.diff(blk[blk >= 0]) > 0)           # fixed (token, slot) order
+
+
+def test_moe_ref_reduces_to_dense():
+    """Identical experts make the grouped GEMM one dense W4A16 GEMM; each expert
+    slice must equal the dense reference on that slice."""
+    rng = np.random.default_rng(7)
+    E, K, N, gs = 4, 64, 32, 32
+    codes = rng.integers(0, 16, (K, N))
+    b = O.pack_k2_uint8(codes)
+    s = O.round_bf16(rng.uniform(0.002, 0.02, (K // gs, N)).astype(np.float32))
+    z = np.full((K // gs, N), 8.0, np.float32)
+    a = O.round_bf16(rng.standard_normal((20, K)).astype(np.float32))
+    offs = np.array([0, 5, 5, 12, 20], np.int32)
+    out = O.moe_w4a16_ref(a, np.stack([b] * E), np.stack([s] * E), np.stack([z] * E), offs, gs)
+    dense = a @ O.w4a16_dequant_weight(b, s, z, gs)
+    np.testing.assert_array_equal(out, dense)
+    codes2 = rng.integers(0, 16, (E, K, N))
+    b2 = np.stack([O.pack_k2_uint8(c) for c in codes2])
+    out2 = O.moe_w4a16_ref(a, b2, np.stack([s] * E), None, offs, gs)
+    for e in range(E):
+        r0, r1 = offs[e], offs[e + 1]
+        ref = a[r0:r1] @ O.w4a16_dequant_weight(b2[e], s, None, gs)
+        np.testing.assert_array_equal(out2[r0:r1], ref)
