@@ -234,6 +234,38 @@ __device__ inline float wave_max(float v) {
 }
 
 // Max over aligned groups of `width` lanes (width a power of two <= 64).
+// Direct global -> LDS copy: lane i's `Bytes` (4 or 16) land at lds + i*Bytes
+// (lds must be the same for the whole wave). Issued as inline asm so the
+// compiler does not treat later LDS reads as depending on it (it would insert
+// a full vmcnt(0) wait before every LDS read, serializing a load ring); the
+// caller orders it explicitly with s_waitcnt vmcnt + s_barrier. M0 is saved
+// and restored around the instruction.
+template <int Bytes>
+__device__ inline void dma_to_lds(const void* gptr, const void* lds) {
+  static_assert(Bytes == 4 || Bytes == 16, "dword or dwordx4");
+  const uint32_t l = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)));
+  uint32_t saved;
+  if constexpr (Bytes == 16)
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+        : "=&s"(saved) : "v"(gptr), "s"(l) : "memory");
+  else
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\t"
+        "global_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
+        : "=&s"(saved) : "v"(gptr), "s"(l) : "memory");
+}
+
+// Workgroup barrier that emits no memory-counter waits of its own (the
+// caller has already waited for what it needs); also a compiler barrier.
+__device__ inline void barrier_no_wait() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 __device__ inline float group_max(float v, int width) {
   for (int o = width >> 1; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
   return v;

@@ -18,6 +18,7 @@
 #include "kernel_set/moe_w4a16.h"
 #include "ks_common.hpp"
 #include "w4a16_mfma.hpp"
+#include "w4a16_pipe.hpp"
 
 namespace ks {
 namespace moe4 {
@@ -61,6 +62,66 @@ moe_mfma_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
     }
     __syncthreads();  // `red` is rewritten by the next pass
   }
+}
+
+// LDS-ring variant (gs % 64 == 0, N % 16 == 0): grid (128-column tiles) x
+// (experts); each workgroup walks its expert's rows in 16*MB-row passes over
+// the whole K of the expert.
+template <typename T, int MB>
+__global__ void __launch_bounds__(w4pipe::kThreads, 2)
+moe_pipe_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
+                const uint8_t* __restrict__ b, const uint16_t* __restrict__ scales,
+                const uint16_t* __restrict__ zeros, const int32_t* __restrict__ offsets,
+                int64_t total_rows, int64_t n, int64_t k, int gs) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int e = blockIdx.y;
+  const int64_t r_begin = min<int64_t>(max<int64_t>(offsets[e], 0), total_rows);
+  const int64_t r_end = min<int64_t>(max<int64_t>(offsets[e + 1], r_begin), total_rows);
+  if (r_end <= r_begin) return;  // uniform across the workgroup
+  const int64_t ng = k / gs;
+  w4pipe::PipeArgs p;
+  p.a = a;
+  p.b = b + static_cast<int64_t>(e) * (k / 2) * n;
+  p.s = scales + static_cast<int64_t>(e) * ng * n;
+  p.z = zeros ? zeros + static_cast<int64_t>(e) * ng * n : nullptr;
+  p.n = n; p.k = k; p.gs = gs;
+  p.n0 = static_cast<int64_t>(blockIdx.x) * w4pipe::kTileN;
+  const int total = static_cast<int>(k / w4pipe::kStageK);
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int li = lane % 16, q = lane / 16;
+  for (int64_t r0 = r_begin; r0 < r_end; r0 += 16 * MB) {
+    w4mma::f32x4 O[MB][2];
+    w4pipe::pipe_tile<T, MB>(p, r0, r_end, 0, total, smem, O);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int64_t col = p.n0 + 32 * wave + 16 * j + li;
+      if (col >= n) continue;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t row = r0 + 16 * mb + 4 * q + r;
+          if (row < r_end) c[row * n + col] = elem<T>::from_f32(O[mb][j][r]);
+        }
+    }
+  }
+}
+
+template <typename T, int MB>
+void launch_pipe(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_t* s,
+                 const uint16_t* z, const int32_t* offs, int E, int64_t rows, int64_t n,
+                 int64_t k, int gs, hipStream_t st) {
+  constexpr int lds = w4pipe::Ring<MB>::kBytes;
+  static bool configured = false;  // opt in to the LDS size once per process
+  if (!configured) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_pipe_kernel<T, MB>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    configured = true;
+  }
+  const dim3 grid(static_cast<unsigned>((n + w4pipe::kTileN - 1) / w4pipe::kTileN),
+                  static_cast<unsigned>(E));
+  hipLaunchKernelGGL((moe_pipe_kernel<T, MB>), grid, dim3(w4pipe::kThreads), lds, st, c, a, b, s,
+                     z, offs, rows, n, k, gs);
 }
 
 // Any-shape fallback: one thread per (row, column); the expert is found by a
@@ -116,8 +177,16 @@ void run(void* c_, const void* a_, const void* b_, const void* s_, const void* z
                        dim3(kThreads), 0, st, c, a, b, s, z, offs, E, rows, n, k, gs);
     return;
   }
-  const dim3 grid(static_cast<unsigned>((n + kTileN - 1) / kTileN), static_cast<unsigned>(E));
   const int64_t avg = (rows + E - 1) / E;
+  const bool pipe = (gs % w4pipe::kStageK == 0) && (n % 16 == 0) && aligned(a, 16) &&
+                    aligned(b, 16) && aligned(s, 4) && aligned(z, 4);
+  if (pipe) {
+    if (avg <= 16) launch_pipe<T, 1>(c, a, b, s, z, offs, E, rows, n, k, gs, st);
+    else if (avg <= 32) launch_pipe<T, 2>(c, a, b, s, z, offs, E, rows, n, k, gs, st);
+    else launch_pipe<T, 4>(c, a, b, s, z, offs, E, rows, n, k, gs, st);
+    return;
+  }
+  const dim3 grid(static_cast<unsigned>((n + kTileN - 1) / kTileN), static_cast<unsigned>(E));
   if (avg <= 16)
     hipLaunchKernelGGL((moe_mfma_kernel<T, 1>), grid, dim3(kThreads), 0, st, c, a, b, s, z, offs, rows, n, k, gs);
   else if (avg <= 32)

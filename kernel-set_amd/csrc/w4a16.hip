@@ -30,6 +30,7 @@
 #include "kernel_set/gemm.h"
 #include "ks_common.hpp"
 #include "w4a16_mfma.hpp"
+#include "w4a16_pipe.hpp"
 #include "workspace.hpp"
 
 namespace ks {
@@ -333,6 +334,99 @@ ks_status_t run_mfma(uint16_t* c, const uint16_t* a, const uint8_t* b, const uin
   return KS_SUCCESS;
 }
 
+// Batched path on the LDS-ring tile: one launch covers rows [row0, row1)
+// (<= 16*MB rows) for every 128-column tile and K split.
+template <typename T, int MB>
+__global__ void __launch_bounds__(w4pipe::kThreads, 2)
+pipe_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
+            const uint8_t* __restrict__ b, const uint16_t* __restrict__ scales,
+            const uint16_t* __restrict__ zeros, const uint16_t* __restrict__ bias,
+            int64_t row0, int64_t row1, int64_t n, int64_t k, int gs, int splits,
+            int stages_per_split, float* __restrict__ ws) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  int tile, split;
+  map_tile(blockIdx.x, gridDim.x, splits, &tile, &split);
+  w4pipe::PipeArgs p;
+  p.a = a; p.b = b; p.s = scales; p.z = zeros;
+  p.n = n; p.k = k; p.gs = gs;
+  p.n0 = static_cast<int64_t>(tile) * w4pipe::kTileN;
+  const int total = static_cast<int>(k / w4pipe::kStageK);
+  const int st0 = split * stages_per_split;
+  const int st1 = min(st0 + stages_per_split, total);
+  w4mma::f32x4 O[MB][2];
+  w4pipe::pipe_tile<T, MB>(p, row0, row1, st0, st1, smem, O);
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int li = lane % 16, q = lane / 16;
+  const int64_t rows = row1 - row0;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int64_t col = p.n0 + 32 * wave + 16 * j + li;
+    if (col >= n) continue;
+    const float bv = (splits == 1 && bias) ? h2f<T>(bias[col]) : 0.f;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t lr = 16 * mb + 4 * q + r;
+        if (lr >= rows) continue;
+        if (splits == 1)
+          c[(row0 + lr) * n + col] = elem<T>::from_f32(O[mb][j][r] + bv);
+        else
+          ws[(static_cast<int64_t>(split) * rows + lr) * n + col] = O[mb][j][r];
+      }
+  }
+}
+
+template <typename T, int MB>
+void launch_pipe(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_t* s,
+                 const uint16_t* z, const uint16_t* bias, int64_t r0, int64_t r1, int64_t n,
+                 int64_t k, int gs, int tiles, int splits, int sps, float* ws, hipStream_t st) {
+  constexpr int lds = w4pipe::Ring<MB>::kBytes;
+  static bool configured = false;  // opt in to the LDS size once per process
+  if (!configured) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&pipe_kernel<T, MB>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    configured = true;
+  }
+  hipLaunchKernelGGL((pipe_kernel<T, MB>), dim3(static_cast<unsigned>(tiles * splits)),
+                     dim3(w4pipe::kThreads), lds, st, c, a, b, s, z, bias, r0, r1, n, k, gs,
+                     splits, sps, ws);
+}
+
+template <typename T>
+ks_status_t run_pipe(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_t* s,
+                     const uint16_t* z, const uint16_t* bias, int64_t m, int64_t n, int64_t k,
+                     int gs, hipStream_t st) {
+  const int tiles = static_cast<int>((n + w4pipe::kTileN - 1) / w4pipe::kTileN);
+  const int total = static_cast<int>(k / w4pipe::kStageK);
+  const int spg = gs / w4pipe::kStageK;
+  // ~512 workgroups (two per CU), splits aligned to quantization groups and at
+  // least 8 stages long so the ring fill is amortized.
+  int splits = std::max(1, (512 + tiles - 1) / tiles);
+  int sps = (total + splits - 1) / splits;
+  sps = std::max(sps, std::min(total, 8));
+  sps = ((sps + spg - 1) / spg) * spg;
+  splits = (total + sps - 1) / sps;
+  const int64_t pass_rows = m > 32 ? 64 : (m > 16 ? 32 : 16);
+  Scratch sc;
+  if (splits > 1) {
+    ks_status_t r = get_scratch(st, static_cast<size_t>(splits) * pass_rows * n, 0, &sc,
+                                "ks_gemm_w4a16");
+    if (r != KS_SUCCESS) return r;
+  }
+  for (int64_t r0 = 0; r0 < m; r0 += pass_rows) {
+    const int64_t r1 = std::min(m, r0 + pass_rows);
+    if (pass_rows == 64)
+      launch_pipe<T, 4>(c, a, b, s, z, bias, r0, r1, n, k, gs, tiles, splits, sps, sc.partial, st);
+    else if (pass_rows == 32)
+      launch_pipe<T, 2>(c, a, b, s, z, bias, r0, r1, n, k, gs, tiles, splits, sps, sc.partial, st);
+    else
+      launch_pipe<T, 1>(c, a, b, s, z, bias, r0, r1, n, k, gs, tiles, splits, sps, sc.partial, st);
+    if (splits > 1) launch_reduce<T>(c + r0 * n, sc.partial, bias, r1 - r0, n, splits, st);
+  }
+  return KS_SUCCESS;
+}
+
 template <typename T, int RPT>
 void launch_gemv(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_t* s,
                  const uint16_t* z, const uint16_t* bias, int m, int n, int k, int gs,
@@ -356,6 +450,10 @@ ks_status_t run(void* c_, const void* a_, const void* b_, const void* s_, const 
 
   const bool mfma = m > kMaxGemvM && (gs % 32 == 0) && (n % 4 == 0) && aligned(a, 16) &&
                     aligned(s, 8) && aligned(z, 8) && aligned(b, 4);
+  const bool pipe = m > kMaxGemvM && (gs % w4pipe::kStageK == 0) && (n % 16 == 0) &&
+                    aligned(a, 16) && aligned(b, 16) && aligned(s, 4) && aligned(z, 4) &&
+                    k * n < (int64_t{1} << 40);
+  if (pipe) return run_pipe<T>(c, a, b, s, z, bias, m, n, k, gs, st);
   if (mfma) return run_mfma<T>(c, a, b, s, z, bias, m, n, k, gs, st);
   const bool vec = (n % 16 == 0) && (gs % 16 == 0) && n <= (int64_t{1} << 30) &&
                    k <= (int64_t{1} << 30) && aligned(b, 16) && aligned(s, 16) &&

@@ -148,7 +148,22 @@ __device__ inline void tile_partial(const TileArgs& p, int64_t r0, float* red /*
                           reinterpret_cast<const uint32_t*>(p.b + (kp + r) * p.n + col))
                     : 0u;
   };
-  if (total_steps > 0) load_w(0, wcur);
+  // Activation fragments are prefetched one step ahead like the weights, so
+  // neither operand's load latency sits on the MFMA chain.
+  uint4 acur[MB], anext[MB];
+  auto load_a = [&](int st, uint4* av) {
+    const int64_t k0 = 2 * (kp_first + static_cast<int64_t>(st) * 16) + 8 * q;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const int64_t row = r0 + 16 * mb + li;
+      av[mb] = (row < p.row1) ? *reinterpret_cast<const uint4*>(p.a + row * p.k + k0)
+                              : make_uint4(0, 0, 0, 0);
+    }
+  };
+  if (total_steps > 0) {
+    load_w(0, wcur);
+    load_a(0, acur);
+  }
 
   f32x4 P[MB][4], S[MB];
   for (int st = 0; st < total_steps; ++st) {
@@ -161,9 +176,11 @@ __device__ inline void tile_partial(const TileArgs& p, int64_t r0, float* red /*
         for (int j = 0; j < 4; ++j) P[mb][j] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
     }
-    if (st + 1 < total_steps) load_w(st + 1, wnext);
+    if (st + 1 < total_steps) {
+      load_w(st + 1, wnext);
+      load_a(st + 1, anext);
+    }
 
-    const int64_t k0 = 2 * (kp_first + static_cast<int64_t>(st) * 16) + 8 * q;
     uint32_t tr[4];
     transpose4x4(wcur, tr);
     u32x4v bf[4];
@@ -172,10 +189,7 @@ __device__ inline void tile_partial(const TileArgs& p, int64_t r0, float* red /*
 
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
-      const int64_t row = r0 + 16 * mb + li;
-      uint4 av = make_uint4(0, 0, 0, 0);
-      if (row < p.row1) av = *reinterpret_cast<const uint4*>(p.a + row * p.k + k0);
-      const u32x4v af = act_frag(av);
+      const u32x4v af = act_frag(acur[mb]);
 #pragma unroll
       for (int j = 0; j < 4; ++j) P[mb][j] = mfma_traits<T>::mma(af, bf[j], P[mb][j]);
       S[mb] = mfma_traits<T>::mma(af, ones, S[mb]);
@@ -221,6 +235,8 @@ __device__ inline void tile_partial(const TileArgs& p, int64_t r0, float* red /*
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) wcur[r] = wnext[r];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acur[mb] = anext[mb];
   }
 
   // ---- cross-wave reduction in a fixed order: waves 1..3 stage, wave 0 sums.
