@@ -281,7 +281,8 @@ def main():
     ap.add_argument("--steps", type=int, default=1024)
     ap.add_argument("--warmup", type=int, default=128)
     ap.add_argument("--rotate", type=int, default=64)
-    ap.add_argument("--only", default="all", help="all | headline")
+    ap.add_argument("--only", default="all",
+                    help="all | headline | comma list of gemm8, quant, w4a16, moe")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--no-graph", action="store_true",
                     help="plain launches with per-call events (for rocprofv3 runs)")
@@ -349,16 +350,21 @@ def main():
                        "GB/s": round(nbytes / (ms_warm * 1e-3) / 1e9, 2)},
     }
 
-    if args.only != "headline":
+    only = set(args.only.split(","))
+    if "all" in only:
+        only = {"gemm8", "quant", "w4a16", "moe"}
+    if only - {"headline"}:
         sec = {}
         steps = max(64, args.steps // 8)
-        fn, per, nb, fl = wl_fp8_gemm(torch, ks, H)
-        ms2, c2 = T.run(fn, per, max(32, steps // 8), 8, min_per_graph=8)
-        sec["fp8_blockwise_gemm_M2048_N7168_K7168"] = line("fp8 gemm", ms2, c2, nb, fl, "mfma", "fp8")
-        fn, per, nb, fl = wl_quant_group(torch, ks, H, 16)
-        ms2, c2 = T.run(fn, per, steps, 32)
-        sec["quant_fp8_group_2048x7168_cold"] = line("quant group", ms2, c2, nb, fl, "hbm")
-        for mm in (1, 16, 64, 256):
+        if "gemm8" in only:
+            fn, per, nb, fl = wl_fp8_gemm(torch, ks, H)
+            ms2, c2 = T.run(fn, per, max(32, steps // 8), 8, min_per_graph=8)
+            sec["fp8_blockwise_gemm_M2048_N7168_K7168"] = line("fp8 gemm", ms2, c2, nb, fl, "mfma", "fp8")
+        if "quant" in only:
+            fn, per, nb, fl = wl_quant_group(torch, ks, H, 16)
+            ms2, c2 = T.run(fn, per, steps, 32)
+            sec["quant_fp8_group_2048x7168_cold"] = line("quant group", ms2, c2, nb, fl, "hbm")
+        for mm in ((1, 16, 64, 256) if "w4a16" in only else ()):
             fn, per, nb, fl = wl_w4a16(torch, ks, H, mm, 4096, 14336, 128, "int69", 16, seed=mm)
             ms2, c2 = T.run(fn, per, steps, 32)
             t_roof = max(nb / (HBM_PEAK_GBS * 1e9), fl / (PEAK_TFLOPS["bf16"] * 1e12))
@@ -366,17 +372,19 @@ def main():
             d["roofline_frac"] = round(t_roof / (ms2 * 1e-3), 4)
             d["bound"] = "hbm" if nb / (HBM_PEAK_GBS * 1e9) >= fl / (PEAK_TFLOPS["bf16"] * 1e12) else "mfma-bf16"
             sec[f"w4a16_M{mm}_K4096_N14336_cold"] = d
-        fn, per, nb, fl = wl_w8a8(torch, ks, H)
-        ms2, c2 = T.run(fn, per, max(32, steps // 8), 8, min_per_graph=8)
-        sec["w8a8_M4096_N4096_K4096"] = line("w8a8", ms2, c2, nb, fl, "mfma", "int8")
-        for K_, N_, nm in ((2048, 1536, "gate_up"), (768, 2048, "down")):
+        if "gemm8" in only:
+            fn, per, nb, fl = wl_w8a8(torch, ks, H)
+            ms2, c2 = T.run(fn, per, max(32, steps // 8), 8, min_per_graph=8)
+            sec["w8a8_M4096_N4096_K4096"] = line("w8a8", ms2, c2, nb, fl, "mfma", "int8")
+        for K_, N_, nm in (((2048, 1536, "gate_up"), (768, 2048, "down")) if "moe" in only else ()):
             fn, per, nb, fl = wl_moe(torch, ks, H, K_, N_, 4)
             ms2, c2 = T.run(fn, per, steps, 16)
             sec[f"moe_w4a16_{nm}_E64_top8_T256_cold"] = line(f"moe {nm}", ms2, c2, nb, fl, "hbm")
         result["secondary"] = sec
-        fp8 = sec["fp8_blockwise_gemm_M2048_N7168_K7168"]
-        result["fp8_gemm_tflops"] = fp8["TFLOP/s"]
-        result["fp8_gemm_frac_of_peak"] = fp8["roofline_frac"]
+        fp8 = sec.get("fp8_blockwise_gemm_M2048_N7168_K7168")
+        if fp8:
+            result["fp8_gemm_tflops"] = fp8["TFLOP/s"]
+            result["fp8_gemm_frac_of_peak"] = fp8["roofline_frac"]
 
     result["cpu_baseline"] = cpu_baseline_w4a16(H, m, k, n, gs, args.cpu_budget)
     print(json.dumps(result), flush=True)

@@ -64,7 +64,7 @@ moe_mfma_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
   }
 }
 
-// LDS-ring variant (gs % 64 == 0, N % 16 == 0): grid (128-column tiles) x
+// LDS-ring variant (gs % 64 == 0, K % 128 == 0, N % 16 == 0): grid (128-column tiles) x
 // (experts); each workgroup walks its expert's rows in 16*MB-row passes over
 // the whole K of the expert.
 template <typename T, int MB>
@@ -178,7 +178,7 @@ void run(void* c_, const void* a_, const void* b_, const void* s_, const void* z
     return;
   }
   const int64_t avg = (rows + E - 1) / E;
-  const bool pipe = (gs % w4pipe::kStageK == 0) && (n % 16 == 0) && aligned(a, 16) &&
+  const bool pipe = (gs % 64 == 0) && (k % w4pipe::kStageK == 0) && (n % 16 == 0) && aligned(a, 16) &&
                     aligned(b, 16) && aligned(s, 4) && aligned(z, 4);
   if (pipe) {
     if (avg <= 16) launch_pipe<T, 1>(c, a, b, s, z, offs, E, rows, n, k, gs, st);

@@ -399,7 +399,7 @@ ks_status_t run_pipe(uint16_t* c, const uint16_t* a, const uint8_t* b, const uin
                      int gs, hipStream_t st) {
   const int tiles = static_cast<int>((n + w4pipe::kTileN - 1) / w4pipe::kTileN);
   const int total = static_cast<int>(k / w4pipe::kStageK);
-  const int spg = gs / w4pipe::kStageK;
+  const int spg = std::max(1, gs / w4pipe::kStageK);  // splits stay on group boundaries
   // ~512 workgroups (two per CU), splits aligned to quantization groups and at
   // least 8 stages long so the ring fill is amortized.
   int splits = std::max(1, (512 + tiles - 1) / tiles);
@@ -450,7 +450,7 @@ ks_status_t run(void* c_, const void* a_, const void* b_, const void* s_, const 
 
   const bool mfma = m > kMaxGemvM && (gs % 32 == 0) && (n % 4 == 0) && aligned(a, 16) &&
                     aligned(s, 8) && aligned(z, 8) && aligned(b, 4);
-  const bool pipe = m > kMaxGemvM && (gs % w4pipe::kStageK == 0) && (n % 16 == 0) &&
+  const bool pipe = m > kMaxGemvM && (gs % 64 == 0) && (k % w4pipe::kStageK == 0) && (n % 16 == 0) &&
                     aligned(a, 16) && aligned(b, 16) && aligned(s, 4) && aligned(z, 4) &&
                     k * n < (int64_t{1} << 40);
   if (pipe) return run_pipe<T>(c, a, b, s, z, bias, m, n, k, gs, st);

@@ -114,3 +114,28 @@ def test_config1_headline_gemv():
 def test_config2_sweep(m):
     # K=4096, N=14336, zeros integer-valued U{6..9}.
     check(m, 4096, 14336, 128, zero_mode="int69", seed=100 + m)
+
+
+@pytest.mark.parametrize("m", [9, 16, 33, 64, 100])
+@pytest.mark.parametrize("k,n,gs", [(1024, 384, 64), (2048, 272, 128), (4096, 512, 256),
+                                    (1536, 256, 512), (960, 256, 64), (1024, 200, 32)])
+def test_batched_shapes(m, k, n, gs):
+    # M > 8 runs on MFMA: the LDS-ring tile when K % 128 == 0, gs % 64 == 0 and
+    # N % 16 == 0 (with N tails, gs = 64 half-stage groups and K splits on
+    # group boundaries), the register tile otherwise.
+    check(m, k, n, gs, seed=m * 3 + k + n + gs)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_batched_dtypes_bias_and_null_zeros(dt):
+    check(24, 1024, 256, 128, dt=dt, bias=True, seed=5)
+    check(40, 1024, 256, 64, zero_mode=None, dt=dt, seed=6)
+    check(70, 2048, 384, 128, zero_mode=None, dt=dt, bias=True, seed=7)
+
+
+def test_batched_deterministic():
+    a, codes, s, z = H.w4a16_inputs(64, 4096, 1024, 128, "int69", seed=8)
+    b = O.pack_k2_uint8(codes)
+    o1, _ = run_w4a16(a, b, s, z, 128)
+    o2, _ = run_w4a16(a, b, s, z, 128)
+    assert np.array_equal(o1, o2)
