@@ -70,12 +70,21 @@ struct Args {
 // Workgroup id -> (tile_m, tile_n). Tiles are walked column-major in groups so
 // that concurrently running workgroups share B column panels in L2.
 __device__ inline void tile_coords(int bid, int tiles_m, int tiles_n, int* tm, int* tn) {
-  constexpr int kGroup = 8;  // tile_m rows per group
+  // Workgroup ids are dispatched round-robin over the 8 XCDs, each with its own
+  // L2. Renumber so every XCD owns a contiguous range of tiles, then walk the
+  // tiles in bands of kGroup tile rows: an XCD's range is then a compact
+  // ~kGroup x (range/kGroup) block whose A and B panels stay in its L2 while
+  // its workgroups move through K together (instead of every XCD streaming
+  // the whole of B).
+  constexpr int kGroup = 4;
+  const int total = tiles_m * tiles_n;
+  int l = bid;
+  if ((total & 7) == 0) l = (bid & 7) * (total >> 3) + (bid >> 3);
   const int per_group = kGroup * tiles_n;
-  const int g = bid / per_group;
+  const int g = l / per_group;
   const int first_m = g * kGroup;
   const int gm = min(tiles_m - first_m, kGroup);
-  const int r = bid % per_group;
+  const int r = l % per_group;
   *tm = first_m + r % gm;
   *tn = r / gm;
 }
@@ -285,6 +294,9 @@ gemm8_kernel(Args p) {
 //    global_load_lds_dwordx4 straight into LDS; every wave instruction fills a
 //    contiguous 1 KB and each lane picks which 16-byte chunk lands in its slot,
 //    which stores both tiles with their chunks XOR-swizzled by (row & 7).
+//    The copies for step s+1 are issued as inline asm before step s's math,
+//    so they overlap it (the compiler would otherwise hold every LDS read of
+//    step s behind them with a vmcnt(0)).
 //  * A fragments: two ds_read_b128 per 16x(32 k) lane slice.
 //  * B fragments are read already transposed with ds_read_b64_tr_b8: in each
 //    16-lane group, lanes (2j, 2j+1) address the two 8-byte halves of k-row j
@@ -355,12 +367,12 @@ gemm8_fast_kernel(Args p) {
     uint8_t* b_dst = sB + buf * kBK * kFBRow + (4 * wave) * 4 * kFBRow;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      __builtin_amdgcn_global_load_lds(p.a + (a_off[i] + k0), a_dst + i * 8 * kFARow, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(p.b + (b_off[i] + k0 * n32), b_dst + i * 4 * kFBRow, 16, 0, 0);
+      dma_to_lds_off<16>(p.a, a_off[i] + k0, a_dst + i * 8 * kFARow);
+      dma_to_lds_off<16>(p.b, b_off[i] + k0 * n32, b_dst + i * 4 * kFBRow);
     }
     if constexpr (kFp8) {  // block_k == 128: K step `step` is scale block `step`
       float* s_dst = (wave < 4) ? sAs + buf * kFBM + 64 * wave : sBs + buf * kFBN + 64 * (wave - 4);
-      __builtin_amdgcn_global_load_lds(s_src + step * s_step, s_dst, 4, 0, 0);
+      dma_to_lds<4>(s_src + step * s_step, s_dst);
     }
   };
 
@@ -408,26 +420,32 @@ gemm8_fast_kernel(Args p) {
         bs[j] = sBs[cur * kFBN + wn + 16 * j + li];
       }
       constexpr int fmt = (KIND == FP8_E5M2) ? 1 : 0;
-      // The MFMAs of row block i are issued before the promotion of row block
-      // i-1, so promotions never wait on a just-issued MFMA.
+      // Software pipeline over the 8 row blocks: the A fragment of block i+1 is
+      // read from LDS while block i's MFMAs run, and block i-1 is promoted
+      // after block i's MFMAs are issued, so neither an LDS read nor a
+      // promotion waits on the instruction just before it.
       f32x4 part[2][4];
       f32x4 scl[2];
       // A fragment: the chunk swizzle (row & 7) equals (li & 7) for every row block.
       const uint8_t* pa0 = a_src + (wm + li) * kFARow;
       const int ca0 = ((2 * lk) ^ (li & 7)) * 16, ca1 = ((2 * lk + 1) ^ (li & 7)) * 16;
+      uint4 xa0 = *reinterpret_cast<const uint4*>(pa0 + ca0);
+      uint4 xa1 = *reinterpret_cast<const uint4*>(pa0 + ca1);
 #pragma unroll
       for (int i = 0; i <= 8; ++i) {
         if (i < 8) {
-          const uint8_t* pa = pa0 + i * 16 * kFARow;
-          const uint4 x0 = *reinterpret_cast<const uint4*>(pa + ca0);
-          const uint4 x1 = *reinterpret_cast<const uint4*>(pa + ca1);
-          const i32x8 fa = i32x8{(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w,
-                                 (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+          const i32x8 fa = i32x8{(int)xa0.x, (int)xa0.y, (int)xa0.z, (int)xa0.w,
+                                 (int)xa1.x, (int)xa1.y, (int)xa1.z, (int)xa1.w};
           scl[i & 1] = *reinterpret_cast<const f32x4*>(&sAs[cur * kFBM + wm + 16 * i + 4 * lk]);
 #pragma unroll
           for (int j = 0; j < 4; ++j)
             part[i & 1][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
                 fa, fb[j], f32x4{0.f, 0.f, 0.f, 0.f}, fmt, fmt, 0, 127, 0, 127);
+          if (i + 1 < 8) {
+            const uint8_t* pa = pa0 + (i + 1) * 16 * kFARow;
+            xa0 = *reinterpret_cast<const uint4*>(pa + ca0);
+            xa1 = *reinterpret_cast<const uint4*>(pa + ca1);
+          }
         }
         if (i > 0) {
           const int ip = i - 1, sp = ip & 1;
@@ -468,8 +486,10 @@ gemm8_fast_kernel(Args p) {
         }
       }
     }
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's loads for step s+1 have landed
-    __syncthreads();
+    // This wave's loads for step s+1 have landed (they were issued as inline
+    // asm, so the compiler does not hold LDS reads of step s behind them).
+    __builtin_amdgcn_s_waitcnt(0);
+    barrier_no_wait();
   }
 
   // ---- epilogue: lane holds rows wm+16i+4lk+r, column wn+16j+li ----

@@ -258,6 +258,26 @@ __device__ inline void dma_to_lds(const void* gptr, const void* lds) {
         : "=&s"(saved) : "v"(gptr), "s"(l) : "memory");
 }
 
+// Same copy addressed as a wave-uniform base plus a 32-bit per-lane byte
+// offset (saddr form): one VGPR per lane instead of a 64-bit address pair.
+template <int Bytes>
+__device__ inline void dma_to_lds_off(const void* sbase, uint32_t voff, const void* lds) {
+  static_assert(Bytes == 4 || Bytes == 16, "dword or dwordx4");
+  const uint32_t l = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)));
+  uint32_t saved;
+  if constexpr (Bytes == 16)
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+        : "=&s"(saved) : "v"(voff), "s"(sbase), "s"(l) : "memory");
+  else
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
+        "global_load_lds_dword %1, %2\n\ts_mov_b32 m0, %0"
+        : "=&s"(saved) : "v"(voff), "s"(sbase), "s"(l) : "memory");
+}
+
 // Workgroup barrier that emits no memory-counter waits of its own (the
 // caller has already waited for what it needs); also a compiler barrier.
 __device__ inline void barrier_no_wait() {
