@@ -14,6 +14,8 @@
 // moves 16 B per lane per load (8 x 16-bit or 2 x 4 x f32), keeps the data it
 // must revisit in registers (one HBM read per element), and reduces amax with
 // wave64 xor-shuffles; scales are written by one lane per group/row.
+#include <type_traits>
+
 #include "kernel_set/quant.h"
 #include "ks_common.hpp"
 
@@ -89,20 +91,63 @@ __device__ inline void store8(uint8_t* dst, const float v[8], float inv) {
 // encode pass share one HBM read. Slots are packed densely over the grid, so a
 // wave covers 64/L consecutive groups of one row (or the tail of one row and
 // the head of the next): 16 B per lane, contiguous across the wave.
+// fp8 codes come from the hardware converters (v_cvt_pk_fp8_f32 /
+// v_cvt_pk_bf8_f32, round to nearest even): every value they see is x * (1/s)
+// with s >= amax/qmax, so |x/s| <= qmax(1 + 2^-23) and both the saturating
+// and the non-saturating conversion give the same code. Index math is 32-bit
+// when the tensor allows it (Idx = uint32_t), with L a compile-time power of 2.
 // ===========================================================================
-template <typename In, typename Enc>
+template <typename Enc>
+struct enc8;
+
+template <>
+struct enc8<e4m3_t> {
+  __device__ static inline uint2 run(const float v[8], float inv) {
+    int lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[0] * inv, v[1] * inv, 0, false);
+    lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[2] * inv, v[3] * inv, lo, true);
+    int hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[4] * inv, v[5] * inv, 0, false);
+    hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[6] * inv, v[7] * inv, hi, true);
+    return make_uint2(static_cast<uint32_t>(lo), static_cast<uint32_t>(hi));
+  }
+};
+
+template <>
+struct enc8<e5m2_t> {
+  __device__ static inline uint2 run(const float v[8], float inv) {
+    int lo = __builtin_amdgcn_cvt_pk_bf8_f32(v[0] * inv, v[1] * inv, 0, false);
+    lo = __builtin_amdgcn_cvt_pk_bf8_f32(v[2] * inv, v[3] * inv, lo, true);
+    int hi = __builtin_amdgcn_cvt_pk_bf8_f32(v[4] * inv, v[5] * inv, 0, false);
+    hi = __builtin_amdgcn_cvt_pk_bf8_f32(v[6] * inv, v[7] * inv, hi, true);
+    return make_uint2(static_cast<uint32_t>(lo), static_cast<uint32_t>(hi));
+  }
+};
+
+template <>
+struct enc8<i8_t> {
+  __device__ static inline uint2 run(const float v[8], float inv) {
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      lo |= static_cast<uint32_t>(i8_t::enc(v[i] * inv)) << (8 * i);
+      hi |= static_cast<uint32_t>(i8_t::enc(v[i + 4] * inv)) << (8 * i);
+    }
+    return make_uint2(lo, hi);
+  }
+};
+
+template <typename In, typename Enc, int LOG_L, typename Idx>
 __global__ void __launch_bounds__(kThreads)
 group_quant_vec_kernel(uint8_t* __restrict__ out, float* __restrict__ scale,
                        const typename In::storage* __restrict__ in,
-                       int64_t rows, int64_t cols, int group_size,
-                       int64_t ngroups, int lanes_per_group) {
-  const int64_t gtid = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-  const int64_t slot = gtid / lanes_per_group;
-  const int sub = static_cast<int>(gtid % lanes_per_group);
+                       Idx rows, Idx cols, Idx group_size, Idx ngroups) {
+  constexpr int L = 1 << LOG_L;
+  const Idx gtid = static_cast<Idx>(blockIdx.x) * kThreads + threadIdx.x;
+  const Idx slot = gtid >> LOG_L;
+  const int sub = static_cast<int>(gtid & (L - 1));
   const bool live_slot = slot < rows * ngroups;
-  const int64_t row = live_slot ? slot / ngroups : 0;
-  const int64_t grp = live_slot ? slot % ngroups : 0;
-  const int64_t col = grp * group_size + static_cast<int64_t>(sub) * 8;
+  const Idx row = live_slot ? slot / ngroups : 0;
+  const Idx grp = live_slot ? slot - row * ngroups : 0;
+  const Idx col = grp * group_size + static_cast<Idx>(sub) * 8;
   const bool live = live_slot && col < cols;
 
   float v[8];
@@ -112,11 +157,11 @@ group_quant_vec_kernel(uint8_t* __restrict__ out, float* __restrict__ scale,
 #pragma unroll
     for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
   }
-  amax = group_max(amax, lanes_per_group);
+  amax = group_max(amax, L);
   const float sc = scale_from_amax<Enc>(amax);
   const float inv = 1.0f / sc;
   if (live) {
-    store8<Enc>(out + row * cols + col, v, inv);
+    *reinterpret_cast<uint2*>(out + row * cols + col) = enc8<Enc>::run(v, inv);
     if (sub == 0) scale[row * ngroups + grp] = sc;
   }
 }
@@ -356,6 +401,11 @@ inline bool aligned(const void* p, uintptr_t a) {
   return (reinterpret_cast<uintptr_t>(p) % a) == 0;
 }
 
+template <typename T>
+struct type_tag {
+  using type = T;
+};
+
 // ---- host launchers (templated on input element and encoder) --------------
 template <typename In, typename Enc>
 void launch_group(uint8_t* out, float* scale, const void* input, int64_t rows,
@@ -368,9 +418,30 @@ void launch_group(uint8_t* out, float* scale, const void* input, int64_t rows,
   if (vec) {
     const int64_t threads = rows * ngroups * lanes;
     const int64_t blocks = (threads + kThreads - 1) / kThreads;
-    hipLaunchKernelGGL((group_quant_vec_kernel<In, Enc>), dim3(static_cast<unsigned>(blocks)),
-                       dim3(kThreads), 0, s, out, scale, static_cast<const S*>(input), rows,
-                       cols, gs, ngroups, lanes);
+    const bool small = blocks * kThreads < (int64_t{1} << 31) && rows * cols < (int64_t{1} << 31);
+    int log_l = 0;
+    while ((1 << log_l) < lanes) ++log_l;
+    auto go = [&](auto log_tag, auto idx_tag) {
+      constexpr int LL = decltype(log_tag)::value;
+      using I = typename decltype(idx_tag)::type;
+      hipLaunchKernelGGL((group_quant_vec_kernel<In, Enc, LL, I>), dim3(static_cast<unsigned>(blocks)),
+                         dim3(kThreads), 0, s, out, scale, static_cast<const S*>(input),
+                         static_cast<I>(rows), static_cast<I>(cols), static_cast<I>(gs),
+                         static_cast<I>(ngroups));
+    };
+    auto by_idx = [&](auto log_tag) {
+      if (small) go(log_tag, type_tag<uint32_t>{});
+      else go(log_tag, type_tag<int64_t>{});
+    };
+    switch (log_l) {
+      case 0: by_idx(std::integral_constant<int, 0>{}); break;
+      case 1: by_idx(std::integral_constant<int, 1>{}); break;
+      case 2: by_idx(std::integral_constant<int, 2>{}); break;
+      case 3: by_idx(std::integral_constant<int, 3>{}); break;
+      case 4: by_idx(std::integral_constant<int, 4>{}); break;
+      case 5: by_idx(std::integral_constant<int, 5>{}); break;
+      default: by_idx(std::integral_constant<int, 6>{}); break;
+    }
   } else {
     const int64_t waves = rows * ngroups;
     const int64_t blocks = (waves * kWave + kThreads - 1) / kThreads;
