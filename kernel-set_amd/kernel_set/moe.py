@@ -1,18 +1,105 @@
-"""Grouped W4A16 GEMM for Mixture-of-Experts (extension, ``moe_w4a16.h``).
+"""Mixture-of-Experts: routing (``moe.h``) and the grouped W4A16 GEMM
+(extension, ``moe_w4a16.h``).
 
-The reference has no quantized grouped GEMM; this follows the argument order of
-its dense ``grouped_gemm`` (``bindings/python/kernel_set/moe.py:189-217``) with
-the weight replaced by the ``gemm_w4a16`` format.
+The routing wrappers keep the reference's names, argument order and return
+values (``bindings/python/kernel_set/moe.py:42-186``). The reference has no
+quantized grouped GEMM; ``grouped_gemm_w4a16`` follows the argument order of
+its dense ``grouped_gemm`` (``moe.py:189-217``) with the weight replaced by the
+``gemm_w4a16`` format.
 """
 from __future__ import annotations
 
-from ctypes import POINTER, c_int32, cast
+from ctypes import POINTER, c_float, c_int32, cast
 from typing import Optional
 
 from ._lib import check, lib
 from ._tensor import TensorLike, default_stream, infer_dtype, ptr
 
-__all__ = ["grouped_gemm_w4a16"]
+__all__ = ["gate_softmax_topk", "gate_sigmoid_group_topk", "compute_permutation", "permute",
+           "unpermute", "grouped_gemm_w4a16"]
+
+
+def _i32(obj, *, name, allow_none=False):
+    return cast(ptr(obj, name=name, allow_none=allow_none), POINTER(c_int32))
+
+
+def _f32(obj, *, name, allow_none=False):
+    return cast(ptr(obj, name=name, allow_none=allow_none), POINTER(c_float))
+
+
+def gate_softmax_topk(out_weights: TensorLike, out_indices: TensorLike, logits: TensorLike,
+                      num_tokens: int, num_experts: int, top_k: int, renormalize: bool = True,
+                      dtype: Optional[int] = None, stream: TensorLike = None):
+    """Softmax over experts then top-k (lowest expert id wins ties).
+
+    logits ``[num_tokens, num_experts]``; out_weights fp32 and out_indices int32
+    ``[num_tokens, top_k]``. Returns ``(out_weights, out_indices)``."""
+    dt = infer_dtype(logits, dtype)
+    check(lib.ks_moe_gate_softmax_topk(
+        _f32(out_weights, name="out_weights"), _i32(out_indices, name="out_indices"),
+        ptr(logits, name="logits"), int(num_tokens), int(num_experts), int(top_k),
+        1 if renormalize else 0, dt, default_stream(stream, logits)),
+        "ks_moe_gate_softmax_topk")
+    return out_weights, out_indices
+
+
+def gate_sigmoid_group_topk(out_weights: TensorLike, out_indices: TensorLike, logits: TensorLike,
+                            num_tokens: int, num_experts: int, n_group: int, topk_group: int,
+                            top_k: int, correction_bias: TensorLike = None,
+                            renormalize: bool = True, routed_scaling_factor: float = 1.0,
+                            dtype: Optional[int] = None, stream: TensorLike = None):
+    """Sigmoid + group-limited top-k gating (DeepSeek-V3 style); ``correction_bias``
+    may be ``None``. Returns ``(out_weights, out_indices)``."""
+    dt = infer_dtype(logits, dtype)
+    check(lib.ks_moe_gate_sigmoid_group_topk(
+        _f32(out_weights, name="out_weights"), _i32(out_indices, name="out_indices"),
+        ptr(logits, name="logits"), ptr(correction_bias, name="correction_bias"),
+        int(num_tokens), int(num_experts), int(n_group), int(topk_group), int(top_k),
+        1 if renormalize else 0, float(routed_scaling_factor), dt,
+        default_stream(stream, logits)),
+        "ks_moe_gate_sigmoid_group_topk")
+    return out_weights, out_indices
+
+
+def compute_permutation(sorted_token_ids: TensorLike, expert_offsets: TensorLike,
+                        topk_indices: TensorLike, num_tokens: int, num_experts: int, top_k: int,
+                        stream: TensorLike = None):
+    """Group the routed pairs ``token*top_k+k`` by expert: sorted_token_ids
+    ``[num_tokens*top_k]`` (pair ids increasing inside each expert), expert_offsets
+    ``[num_experts+1]``. Returns ``(sorted_token_ids, expert_offsets)``."""
+    check(lib.ks_moe_compute_permutation(
+        _i32(sorted_token_ids, name="sorted_token_ids"), _i32(expert_offsets, name="expert_offsets"),
+        _i32(topk_indices, name="topk_indices"), int(num_tokens), int(num_experts), int(top_k),
+        default_stream(stream, topk_indices)),
+        "ks_moe_compute_permutation")
+    return sorted_token_ids, expert_offsets
+
+
+def permute(permuted: TensorLike, input: TensorLike, sorted_token_ids: TensorLike,
+            num_tokens: int, top_k: int, hidden: int, dtype: Optional[int] = None,
+            stream: TensorLike = None) -> TensorLike:
+    """``permuted[r] = input[sorted_token_ids[r] // top_k]``."""
+    dt = infer_dtype(input, dtype)
+    check(lib.ks_moe_permute(
+        ptr(permuted, name="permuted"), ptr(input, name="input"),
+        _i32(sorted_token_ids, name="sorted_token_ids"), int(num_tokens), int(top_k),
+        int(hidden), dt, default_stream(stream, input)),
+        "ks_moe_permute")
+    return permuted
+
+
+def unpermute(out: TensorLike, permuted: TensorLike, sorted_token_ids: TensorLike,
+              routing_weights: TensorLike, num_tokens: int, top_k: int, hidden: int,
+              dtype: Optional[int] = None, stream: TensorLike = None) -> TensorLike:
+    """``out[token] = sum_k weight[token,k] * permuted[pos(token,k)]`` (fp32, k order)."""
+    dt = infer_dtype(permuted, dtype)
+    check(lib.ks_moe_unpermute(
+        ptr(out, name="out"), ptr(permuted, name="permuted"),
+        _i32(sorted_token_ids, name="sorted_token_ids"),
+        _f32(routing_weights, name="routing_weights"), int(num_tokens), int(top_k), int(hidden),
+        dt, default_stream(stream, permuted)),
+        "ks_moe_unpermute")
+    return out
 
 
 def grouped_gemm_w4a16(c: TensorLike, a: TensorLike, b_packed: TensorLike,

@@ -383,3 +383,145 @@ def moe_w4a16_ref(a, b_packed, scales, zeros, offsets, group_size, dtype="bf16")
                                      None if zeros is None else zeros[e], group_size, dtype)
             out[r0:r1] = a[r0:r1] @ w
     return out
+
+
+# ---------------------------------------------------------------------------
+# MoE routing (gates, permutation, permute, unpermute)
+# ---------------------------------------------------------------------------
+_NEG_MAX = np.float32(-3.4028235e38)
+
+
+def gate_softmax_topk_ref(logits, top_k: int, renormalize: bool = True):
+    """moe_gate.cu:42-117: fp32 softmax (max-shifted), then top_k picks by a
+    strict '>' scan in increasing expert id (lowest id wins ties); the chosen
+    probabilities are divided by their sum (summed in pick order) when
+    renormalize is set. Returns (weights fp32 [T, k], indices int32 [T, k])."""
+    x = _c(logits, np.float32)
+    T, E = x.shape
+    w = np.zeros((T, top_k), np.float32)
+    idx = np.zeros((T, top_k), np.int32)
+    for t in range(T):
+        p = np.exp(x[t] - x[t].max()).astype(np.float32)
+        s = np.float32(0)
+        for v in p:
+            s = np.float32(s + v)
+        prob = (p * np.float32(np.float32(1) / s)).astype(np.float32)
+        order = np.argsort(-prob, kind="stable")[:top_k]
+        renorm = np.float32(0)
+        for v in prob[order]:
+            renorm = np.float32(renorm + v)
+        scale = np.float32(1) / renorm if (renormalize and renorm > 0) else np.float32(1)
+        w[t] = prob[order] * scale
+        idx[t] = order
+    return w, idx
+
+
+def _sigmoid32(x):
+    x = np.float32(x)
+    if x >= 0:
+        return np.float32(np.float32(1) / (np.float32(1) + np.float32(np.exp(-x))))
+    z = np.float32(np.exp(x))
+    return np.float32(z / (np.float32(1) + z))
+
+
+def gate_sigmoid_group_topk_ref(logits, bias, n_group: int, topk_group: int, top_k: int,
+                                renormalize: bool = True, routed_scaling_factor: float = 1.0):
+    """moe_gate.cu:119-236 (DeepSeek-V3 grouped top-k), restated as the
+    reference's sequential loops: group score = sum of the group's two best
+    biased scores, the topk_group best groups survive (strict '>' in group
+    order), top_k experts of the survivors by biased score (strict '>', expert
+    order); weights are the unbiased sigmoid scores, renormalized, times the
+    routed scaling factor. Missing picks get id 0 and weight 0."""
+    x = _c(logits, np.float32)
+    T, E = x.shape
+    b = None if bias is None else _c(bias, np.float32)
+    epg = E // n_group
+    w = np.zeros((T, top_k), np.float32)
+    idx = np.zeros((T, top_k), np.int32)
+    for t in range(T):
+        score = np.array([_sigmoid32(v) for v in x[t]], np.float32)
+        sel = score.copy() if b is None else (score + b).astype(np.float32)
+        gsc = []
+        for g in range(n_group):
+            m1 = m2 = _NEG_MAX
+            for v in sel[g * epg:(g + 1) * epg]:
+                if v > m1:
+                    m1, m2 = v, m1
+                elif v > m2:
+                    m2 = v
+            gsc.append(np.float32(m1 + m2) if epg >= 2 else m1)
+        keep = [False] * n_group
+        tmp = list(gsc)
+        for _ in range(min(topk_group, n_group)):
+            best, bg = _NEG_MAX, -1
+            for g in range(n_group):
+                if tmp[g] > best:
+                    best, bg = tmp[g], g
+            if bg < 0:
+                break
+            keep[bg] = True
+            tmp[bg] = _NEG_MAX
+        renorm = np.float32(0)
+        for k in range(top_k):
+            best, be = _NEG_MAX, -1
+            for e in range(E):
+                if keep[e // epg] and sel[e] > best:
+                    best, be = sel[e], e
+            if be < 0:
+                continue
+            w[t, k], idx[t, k] = score[be], be
+            renorm = np.float32(renorm + score[be])
+            sel[be] = _NEG_MAX
+        norm = np.float32(1) / renorm if (renormalize and renorm > 0) else np.float32(1)
+        w[t] = (w[t] * norm * np.float32(routed_scaling_factor)).astype(np.float32)
+    return w, idx
+
+
+def compute_permutation_ref(topk_ids, num_experts: int):
+    """moe_permute.cu:58-101 as a stable counting sort: pairs (token*top_k+k)
+    grouped by expert in increasing pair id; out-of-range ids are dropped.
+    Returns (sorted_ids int32 [valid pairs], offsets int32 [E+1])."""
+    flat = _c(topk_ids, np.int32).reshape(-1)
+    ok = (flat >= 0) & (flat < num_experts)
+    pairs = np.nonzero(ok)[0]
+    order = pairs[np.argsort(flat[pairs], kind="stable")]
+    counts = np.bincount(flat[pairs], minlength=num_experts)
+    offs = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    return order.astype(np.int32), offs
+
+
+def permute_ref(x, sorted_ids, top_k: int):
+    """moe_permute.cu:103-129: row r = x[sorted_ids[r] // top_k], zero when the
+    id is out of range."""
+    x = np.asarray(x)
+    rows = len(sorted_ids)
+    out = np.zeros((rows, x.shape[1]), x.dtype)
+    for r, pr in enumerate(np.asarray(sorted_ids, np.int64)):
+        if 0 <= pr < rows:
+            out[r] = x[pr // top_k]
+    return out
+
+
+def unpermute_ref(permuted, sorted_ids, weights, num_tokens: int, top_k: int):
+    """moe_permute.cu:131-170: out[t] = sum_k w[t,k] * permuted[inv[t*top_k+k]]
+    accumulated in fp32 in increasing k with a fused multiply-add (each step
+    rounded once, computed exactly in float64 then rounded), absent pairs
+    skipped."""
+    p = _c(permuted, np.float32)
+    rows = len(sorted_ids)
+    inv = np.full(rows, -1, np.int64)
+    for r, pr in enumerate(np.asarray(sorted_ids, np.int64)):
+        if 0 <= pr < rows:
+            inv[pr] = r
+    wt = _c(weights, np.float32).reshape(-1)
+    out = np.zeros((num_tokens, p.shape[1]), np.float32)
+    for t in range(num_tokens):
+        acc = np.zeros(p.shape[1], np.float32)
+        for k in range(top_k):
+            r = inv[t * top_k + k]
+            if r < 0:
+                continue
+            acc = (p[r].astype(np.float64) * np.float64(wt[t * top_k + k])
+                   + acc.astype(np.float64)).astype(np.float32)
+        out[t] = acc
+    return out

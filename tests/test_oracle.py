@@ -311,3 +311,80 @@ def test_moe_ref_reduces_to_dense():
         r0, r1 = offs[e], offs[e + 1]
         ref = a[r0:r1] @ O.w4a16_dequant_weight(b2[e], s, None, gs)
         np.testing.assert_array_equal(out2[r0:r1], ref)
+
+
+def test_gate_softmax_ref_brute_force_and_ties():
+    rng = np.random.default_rng(21)
+    lg = rng.standard_normal((30, 16)).astype(np.float32)
+    lg[0, [2, 5, 11]] = 4.0
+    lg[1, :] = 0.5
+    w, idx = O.gate_softmax_topk_ref(lg, 4, renormalize=True)
+    assert list(idx[0][:3]) == [2, 5, 11] and list(idx[1]) == [0, 1, 2, 3]
+    np.testing.assert_allclose(w.sum(1), 1.0, rtol=1e-6)
+    w2, idx2 = O.gate_softmax_topk_ref(lg, 4, renormalize=False)
+    assert np.array_equal(idx, idx2)
+    for t in range(lg.shape[0]):
+        p = np.exp(lg[t].astype(np.float64) - lg[t].max())
+        p /= p.sum()
+        best = sorted(range(16), key=lambda e: (-float(np.float32(p[e])), e))[:4]
+        assert list(idx2[t]) == best
+        np.testing.assert_allclose(w2[t], p[best], rtol=1e-6)
+
+
+def _grouped_topk_vectorized(lg, bias, n_group, topk_group, top_k, rsf):
+    """Independent formulation (sorting instead of scans) for cross-checking."""
+    T, E = lg.shape
+    epg = E // n_group
+    score = 1.0 / (1.0 + np.exp(-lg.astype(np.float64)))
+    sel = score + (0 if bias is None else bias.astype(np.float64))
+    out_w, out_i = [], []
+    for t in range(T):
+        g = sel[t].reshape(n_group, epg)
+        top2 = np.sort(g, axis=1)[:, ::-1][:, :2].sum(1) if epg >= 2 else g[:, 0]
+        groups = sorted(range(n_group), key=lambda j: (-top2[j], j))[:topk_group]
+        cand = [e for e in range(E) if e // epg in groups]
+        pick = sorted(cand, key=lambda e: (-sel[t, e], e))[:top_k]
+        ww = score[t, pick]
+        out_w.append(ww / ww.sum() * rsf)
+        out_i.append(pick)
+    return np.array(out_w), np.array(out_i)
+
+
+@pytest.mark.parametrize("E,ng,tg,k,bias", [(32, 4, 2, 4, True), (64, 8, 3, 6, False),
+                                            (16, 1, 1, 5, True), (24, 24, 6, 3, False)])
+def test_gate_sigmoid_group_ref_two_ways(E, ng, tg, k, bias):
+    rng = np.random.default_rng(E + k)
+    lg = rng.standard_normal((12, E)).astype(np.float32)
+    b = rng.uniform(-0.3, 0.3, E).astype(np.float32) if bias else None
+    w, idx = O.gate_sigmoid_group_topk_ref(lg, b, ng, tg, k, True, 2.5)
+    w2, idx2 = _grouped_topk_vectorized(lg, b, ng, tg, k, 2.5)
+    assert np.array_equal(idx, idx2)
+    np.testing.assert_allclose(w, w2, rtol=1e-5)
+
+
+def test_permutation_ref_matches_grouping_and_drops_invalid():
+    rng = np.random.default_rng(22)
+    ids = O.moe_topk_ids(rng.standard_normal((40, 12)).astype(np.float32), 3)
+    srt, offs = O.compute_permutation_ref(ids, 12)
+    row_src, offs2 = O.moe_group_rows(ids, 12, 1)
+    assert np.array_equal(srt, row_src) and np.array_equal(offs, offs2)
+    bad = ids.copy()
+    bad[0, 0], bad[5, 2] = -1, 12
+    srt, offs = O.compute_permutation_ref(bad, 12)
+    assert offs[-1] == ids.size - 2 and 0 not in srt.tolist() and 17 not in srt.tolist()
+
+
+def test_unpermute_ref_closed_forms():
+    rng = np.random.default_rng(23)
+    T, k, H = 6, 2, 8
+    perm = O.round_bf16(rng.standard_normal((T * k, H)).astype(np.float32))
+    ident = np.arange(T * k, dtype=np.int32)
+    onehot = np.zeros((T, k), np.float32)
+    onehot[:, 1] = 1.0
+    out = O.unpermute_ref(perm, ident, onehot, T, k)
+    assert np.array_equal(out, perm[1::2])
+    x = O.round_bf16(rng.standard_normal((T, H)).astype(np.float32))
+    p = O.permute_ref(x, ident, k)
+    assert np.array_equal(p[::2], x) and np.array_equal(p[1::2], x)
+    half = np.full((T, k), 0.5, np.float32)
+    assert np.array_equal(O.unpermute_ref(p, ident, half, T, k), x)
