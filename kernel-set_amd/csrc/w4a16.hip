@@ -31,6 +31,7 @@
 #include "ks_common.hpp"
 #include "w4a16_mfma.hpp"
 #include "w4a16_pipe.hpp"
+#include "w4a16_dq.hpp"
 #include "workspace.hpp"
 
 namespace ks {
@@ -41,6 +42,7 @@ constexpr int kLanesN = 8;                    // lanes across the column tile
 constexpr int kTileN = kLanesN * 16;          // 128 columns per workgroup
 constexpr int kRowsPar = kThreads / kLanesN;  // 32 row lanes
 constexpr int kMaxGemvM = 8;
+constexpr int kDqMinM = 64;  // above this M the dequantize-to-LDS MFMA GEMM runs (measured crossover)
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
@@ -427,6 +429,23 @@ ks_status_t run_pipe(uint16_t* c, const uint16_t* a, const uint8_t* b, const uin
   return KS_SUCCESS;
 }
 
+// Larger M: weights dequantized once per workgroup into LDS, 32x32x16 MFMA.
+template <typename T, int BM, int BN>
+void launch_dq(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_t* s,
+               const uint16_t* z, const uint16_t* bias, int64_t m, int64_t n, int64_t k, int gs,
+               hipStream_t st) {
+  using C = w4dq::Cfg<BM, BN>;
+  static bool configured = false;  // opt in to the LDS size once per process
+  if (!configured) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&w4dq::dq_kernel<T, BM, BN>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, C::kBytes);
+    configured = true;
+  }
+  const dim3 grid(static_cast<unsigned>(n / BN), static_cast<unsigned>((m + BM - 1) / BM));
+  hipLaunchKernelGGL((w4dq::dq_kernel<T, BM, BN>), grid, dim3(C::kThreads), C::kBytes, st, c, a, b,
+                     s, z, bias, m, n, k, gs);
+}
+
 template <typename T, int RPT>
 void launch_gemv(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_t* s,
                  const uint16_t* z, const uint16_t* bias, int m, int n, int k, int gs,
@@ -453,6 +472,20 @@ ks_status_t run(void* c_, const void* a_, const void* b_, const void* s_, const 
   const bool pipe = m > kMaxGemvM && (gs % 64 == 0) && (k % w4pipe::kStageK == 0) && (n % 16 == 0) &&
                     aligned(a, 16) && aligned(b, 16) && aligned(s, 4) && aligned(z, 4) &&
                     k * n < (int64_t{1} << 40);
+  const bool dq = m > kDqMinM && (gs % 64 == 0) && (k % 64 == 0) && (n % 64 == 0) &&
+                  aligned(a, 16) && aligned(b, 16) && aligned(s, 4) && aligned(z, 4) &&
+                  (m + 127) / 128 < 65536;
+  if (dq) {
+    const bool wide = n % 128 == 0;
+    if (m > 64) {
+      if (wide) launch_dq<T, 128, 128>(c, a, b, s, z, bias, m, n, k, gs, st);
+      else launch_dq<T, 128, 64>(c, a, b, s, z, bias, m, n, k, gs, st);
+    } else {
+      if (wide) launch_dq<T, 64, 128>(c, a, b, s, z, bias, m, n, k, gs, st);
+      else launch_dq<T, 64, 64>(c, a, b, s, z, bias, m, n, k, gs, st);
+    }
+    return KS_SUCCESS;
+  }
   if (pipe) return run_pipe<T>(c, a, b, s, z, bias, m, n, k, gs, st);
   if (mfma) return run_mfma<T>(c, a, b, s, z, bias, m, n, k, gs, st);
   const bool vec = (n % 16 == 0) && (gs % 16 == 0) && n <= (int64_t{1} << 30) &&

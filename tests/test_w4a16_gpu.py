@@ -116,13 +116,15 @@ def test_config2_sweep(m):
     check(m, 4096, 14336, 128, zero_mode="int69", seed=100 + m)
 
 
-@pytest.mark.parametrize("m", [9, 16, 33, 64, 100])
+@pytest.mark.parametrize("m", [9, 16, 33, 64, 100, 257])
 @pytest.mark.parametrize("k,n,gs", [(1024, 384, 64), (2048, 272, 128), (4096, 512, 256),
-                                    (1536, 256, 512), (960, 256, 64), (1024, 200, 32)])
+                                    (1536, 256, 512), (960, 256, 64), (1024, 200, 32),
+                                    (1024, 448, 128)])
 def test_batched_shapes(m, k, n, gs):
-    # M > 8 runs on MFMA: the LDS-ring tile when K % 128 == 0, gs % 64 == 0 and
-    # N % 16 == 0 (with N tails, gs = 64 half-stage groups and K splits on
-    # group boundaries), the register tile otherwise.
+    # M > 8 runs on MFMA: for M > 64 with N % 64 == 0 the dequantize-to-LDS
+    # GEMM (64- or 128-column tiles), otherwise the LDS-ring tile when
+    # K % 128 == 0, gs % 64 == 0 and N % 16 == 0 (with N tails, gs = 64
+    # half-stage groups and K splits on group boundaries), else the register tile.
     check(m, k, n, gs, seed=m * 3 + k + n + gs)
 
 
