@@ -344,7 +344,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(),
-                     "kernel": "ks_gemm_w4a16 call = ks::w4a16::gemv_kernel + reduce_kernel",
+                     "kernel": "ks_gemm_w4a16 call = ks::w4dec::dec_kernel + ks::w4a16::dec_reduce_kernel",
                      "bytes_per_launch": nbytes},
         "warm_cache": {"us_per_call": round(ms_warm * 1e3, 3),
                        "GB/s": round(nbytes / (ms_warm * 1e-3) / 1e9, 2)},

@@ -6,17 +6,19 @@
 //   low nibble), scales/zeros/A/C/bias all in the activation dtype, fp32 math,
 //   output rounded to nearest even.
 //
-// Decode path (M <= 8), HBM-bound. Measured on MI355X: reading the weight
-// stream reaches full bandwidth only when each workgroup reads whole 128-byte
-// lines of consecutive packed rows (column strips narrower than a line read
-// ~2x slower), so a workgroup owns a 128-column x 32*RPT-row tile and K is
-// split over S workgroups. Cross-workgroup reduction inside one kernel needs an
-// agent-scope release (an L2 writeback per workgroup on this chip), which
-// costs more than a second launch, so the split partials go to a scratch plane
-// and a small reduce kernel sums them in a fixed order (deterministic) and
-// adds the bias.
+// Decode path (M <= 8), HBM-bound: w4a16_dec.hpp (MFMA, no byte transpose)
+// when gs % 32 == 0 and the operands are 16-byte aligned; the dot2 kernel
+// below otherwise. Measured on MI355X: reading the weight stream reaches full
+// bandwidth only when each workgroup reads whole 128-byte lines of consecutive
+// packed rows (column strips narrower than a line read ~2x slower), so K is
+// split over workgroups. A cross-workgroup reduction inside one kernel
+// (last-arriver, through L2 or device-coherent memory, or fp32 atomics)
+// measured slower than a second launch, so the split partials go to a scratch
+// plane and a small reduce kernel sums them in a fixed order (deterministic)
+// and adds the bias. The decode reduce runs each tile on the XCD that wrote
+// its partials, which reads them from that XCD's L2.
 //
-// Inner loop: v_dot2_f32_bf16 (or _f16). The activation pair (a[2kp],
+// dot2 fallback: v_dot2_f32_bf16 (or _f16). The activation pair (a[2kp],
 // a[2kp+1]) is used as loaded; each packed byte becomes the 16-bit float pair
 // (base + q_even, base + q_odd) with two v_perm ops per 4 columns
 // (bf16 0x4300|q = 128 + q; f16 0x5800|q = 128 + q/8, both exact), so
@@ -32,6 +34,7 @@
 #include "w4a16_mfma.hpp"
 #include "w4a16_pipe.hpp"
 #include "w4a16_dq.hpp"
+#include "w4a16_dec.hpp"
 #include "workspace.hpp"
 
 namespace ks {
@@ -457,6 +460,93 @@ void launch_gemv(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_
   else hipLaunchKernelGGL((gemv_kernel<T, 8, RPT>), grid, block, 0, st, c, a, b, s, z, bias, m, n, k, gs, splits, ws);
 }
 
+// Split-plane reduce for the decode kernel: one workgroup per 256-column tile,
+// placed on the XCD whose workgroups wrote that tile's partials (workgroup ids
+// are dispatched to the 8 XCDs round-robin), so the planes are read from that
+// XCD's L2. Sums in split order, + bias.
+template <typename T>
+__global__ void __launch_bounds__(w4dec::kTileN)
+dec_reduce_kernel(uint16_t* __restrict__ c, const float* __restrict__ ws,
+                  const uint16_t* __restrict__ bias, int rows, int n, int splits, int tiles) {
+  int tile = blockIdx.x;
+  if ((tiles & 7) == 0) tile = (blockIdx.x & 7) * (tiles >> 3) + (blockIdx.x >> 3);
+  const int col = tile * w4dec::kTileN + threadIdx.x;
+  if (col >= n) return;
+  const int64_t plane = static_cast<int64_t>(rows) * n;
+  const float bv = bias ? h2f<T>(bias[col]) : 0.f;
+  for (int m = 0; m < rows; ++m) {
+    const float* p = ws + static_cast<int64_t>(m) * n + col;
+    float part[8];
+    float o = 0.f;
+    int sp = 0;
+    for (; sp + 8 <= splits; sp += 8) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) part[i] = p[(sp + i) * plane];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o += part[i];
+    }
+    for (; sp < splits; ++sp) o += p[sp * plane];
+    c[static_cast<int64_t>(m) * n + col] = elem<T>::from_f32(o + bv);
+  }
+}
+
+template <typename T, int MB, int WAVES, int RPT>
+void launch_dec(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_t* s,
+                const uint16_t* z, const uint16_t* bias, int m, int n, int k, int gs, int tiles,
+                int splits, float* ws, hipStream_t st) {
+  hipLaunchKernelGGL((w4dec::dec_kernel<T, MB, WAVES, RPT>), dim3(tiles * splits),
+                     dim3(64 * WAVES), 0, st, c, a, b, s, z, bias, m, n, k,
+                     gs, splits, ws);
+}
+
+template <typename T, int WAVES, int RPT>
+ks_status_t dec_rows(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_t* s,
+                     const uint16_t* z, const uint16_t* bias, int64_t m, int64_t n, int64_t k,
+                     int gs, hipStream_t st) {
+  const int tiles = static_cast<int>((n + w4dec::kTileN - 1) / w4dec::kTileN);
+  const int rows_wg = w4dec::Geo<WAVES, RPT>::kRowsWG;
+  const int splits = static_cast<int>((k / 2 + rows_wg - 1) / rows_wg);
+  Scratch sc;
+  if (splits > 1) {
+    ks_status_t r = get_scratch(st, static_cast<size_t>(splits) * kMaxGemvM * n, 0, &sc,
+                                "ks_gemm_w4a16");
+    if (r != KS_SUCCESS) return r;
+  }
+  const int ni = static_cast<int>(n), ki = static_cast<int>(k), mi = static_cast<int>(m);
+  if (m <= 4)
+    launch_dec<T, 1, WAVES, RPT>(c, a, b, s, z, bias, mi, ni, ki, gs, tiles, splits, sc.partial, st);
+  else
+    launch_dec<T, 2, WAVES, RPT>(c, a, b, s, z, bias, mi, ni, ki, gs, tiles, splits, sc.partial, st);
+  if (splits > 1)
+    hipLaunchKernelGGL((dec_reduce_kernel<T>), dim3(tiles), dim3(w4dec::kTileN), 0, st, c,
+                       sc.partial, bias, mi, ni, splits, tiles);
+  return KS_SUCCESS;
+}
+
+// Decode shapes (M <= 8) on MFMA; returns false when the shape or alignment
+// does not fit the kernel's requirements.
+template <typename T>
+bool run_dec(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_t* s,
+             const uint16_t* z, const uint16_t* bias, int64_t m, int64_t n, int64_t k, int gs,
+             hipStream_t st, ks_status_t* r) {
+  if (n % 16 != 0 || k % 8 != 0 || n > (int64_t{1} << 30) || k > (int64_t{1} << 30) ||
+      !aligned(a, 16) ||
+      !aligned(b, 16) || !aligned(s, 16) || !aligned(z, 16))
+    return false;
+  // Measured on MI355X at M=1 K=N=4096: 4 waves x 8 rows per lane (256
+  // workgroups, 16 splits) beats 8 waves x 4 rows, 4 waves x 4 rows and
+  // 8 waves x 8 rows (fewer workgroups).
+  if (gs % 64 == 0 && k % 64 == 0) {
+    *r = dec_rows<T, 4, 8>(c, a, b, s, z, bias, m, n, k, gs, st);
+    return true;
+  }
+  if (gs % 32 == 0 && k % 32 == 0) {
+    *r = dec_rows<T, 4, 4>(c, a, b, s, z, bias, m, n, k, gs, st);
+    return true;
+  }
+  return false;
+}
+
 template <typename T>
 ks_status_t run(void* c_, const void* a_, const void* b_, const void* s_, const void* z_,
                 const void* bias_, int64_t m, int64_t n, int64_t k, int gs, hipStream_t st) {
@@ -496,6 +586,10 @@ ks_status_t run(void* c_, const void* a_, const void* b_, const void* s_, const 
                                                 static_cast<unsigned>(m)),
                        dim3(kThreads), 0, st, c, a, b, s, z, bias, n, k, gs);
     return KS_SUCCESS;
+  }
+  if (m <= kMaxGemvM) {
+    ks_status_t r;
+    if (run_dec<T>(c, a, b, s, z, bias, m, n, k, gs, st, &r)) return r;
   }
   const int tiles = static_cast<int>((n + kTileN - 1) / kTileN);
   const int64_t kp = k / 2;

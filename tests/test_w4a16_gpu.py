@@ -46,7 +46,9 @@ def check(m, k, n, gs, zero_mode="int69", dt="bf16", seed=0, bias=False):
 
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8])
 @pytest.mark.parametrize("k,n,gs", [(256, 128, 128), (512, 384, 64), (1024, 272, 32),
-                                    (4096, 4096, 128), (2048, 1040, 256)])
+                                    (4096, 4096, 128), (2048, 1040, 256),
+                                    # K/2 not a multiple of a workgroup's rows, N not of 256
+                                    (320, 528, 64), (160, 96, 32)])
 def test_gemv_shapes(m, k, n, gs):
     check(m, k, n, gs, seed=m * 7 + k + n)
 
