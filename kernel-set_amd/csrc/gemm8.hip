@@ -293,7 +293,7 @@ gemm8_kernel(Args p) {
 //  * A [256 rows][128 B] and B [128 k][256 n] tiles are fetched with
 //    global_load_lds_dwordx4 straight into LDS; every wave instruction fills a
 //    contiguous 1 KB and each lane picks which 16-byte chunk lands in its slot,
-//    which stores both tiles with their chunks XOR-swizzled by (row & 7).
+//    which stores both tiles with their chunks XOR-swizzled (a_swz, b_swz).
 //    The copies for step s+1 are issued as inline asm before step s's math,
 //    so they overlap it (the compiler would otherwise hold every LDS read of
 //    step s behind them with a vmcnt(0)).
@@ -301,8 +301,7 @@ gemm8_kernel(Args p) {
 //  * B fragments are read already transposed with ds_read_b64_tr_b8: in each
 //    16-lane group, lanes (2j, 2j+1) address the two 8-byte halves of k-row j
 //    of a 16-column block and lane i receives column i of those 8 rows, i.e.
-//    8 consecutive k of one column, the MFMA operand order. With the swizzle
-//    the 16 reads of a group touch 16 distinct 8-byte bank slots.
+//    8 consecutive k of one column, the MFMA operand order.
 //  * fp8 (block_k == 128): each 16x16x128 MFMA is one whole scale block, so the
 //    partial is promoted at once: O = fma(P, a_s * b_s, O). The two scale
 //    vectors of a step are also fetched straight into LDS.
@@ -313,6 +312,16 @@ constexpr int kFARow = 128;  // bytes per A row in LDS
 constexpr int kFBRow = 256;  // bytes per B k-row in LDS
 
 typedef int i32x2 __attribute__((ext_vector_type(2)));
+
+// LDS chunk swizzles (gfx950 LDS: 64 banks x 4 B, so 256 bytes per bank cycle).
+// A rows are 128 B: rows r and r+2 share a bank range, so the 16 rows of a
+// 16-lane fragment read (r = 0..15) get distinct chunks from (r >> 1) & 7.
+// B k-rows are 256 B (every row starts at bank 0): the 8 rows of one transposed
+// read get distinct chunks from r & 7, and bit 3 of the chunk flips between the
+// two 16-lane groups that read in the same cycle (rows 32 apart for fp8, 16
+// apart for int8).
+__device__ inline int a_swz(int row) { return (row >> 1) & 7; }
+__device__ inline int b_swz(int row) { return (row & 7) | ((((row >> 4) ^ (row >> 5)) & 1) << 3); }
 typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
 
 template <int KIND, typename Out, bool UNIFORM_BS>
@@ -346,9 +355,9 @@ gemm8_fast_kernel(Args p) {
   for (int i = 0; i < 4; ++i) {
     const int row = 8 * (4 * wave + i) + lane / 8;
     const int64_t gm = min<int64_t>(m0 + row, p.m - 1);  // rows past M are never stored
-    a_off[i] = static_cast<uint32_t>(gm * p.k + 16 * ((lane % 8) ^ (row & 7)));
+    a_off[i] = static_cast<uint32_t>(gm * p.k + 16 * ((lane % 8) ^ a_swz(row)));
     const int krow = 4 * (4 * wave + i) + lane / 16;       // B: 4 k-rows per instruction
-    b_off[i] = static_cast<uint32_t>(krow * p.n + n0 + 16 * ((lane % 16) ^ (krow & 7)));
+    b_off[i] = static_cast<uint32_t>(krow * p.n + n0 + 16 * ((lane % 16) ^ b_swz(krow)));
   }
   const uint32_t n32 = static_cast<uint32_t>(p.n);
   // scales: waves 0-3 fetch a_scale of rows 64*wave+lane, waves 4-7 b_scale
@@ -390,6 +399,14 @@ gemm8_fast_kernel(Args p) {
   // k-row (kbase + jj), bytes 8h..8h+7 of the 16-column block.
   const int tr_jj = li >> 1, tr_h = li & 1;
 
+  // fp8: the last two partials of a step are promoted at the start of the next.
+  f32x4 plast[2], sclast;
+  float bslast[4];
+  auto promote16 = [](f32x4& o, const f32x4& part, const f32x4& sc) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) o[r] = fmaf(part[r], sc[r], o[r]);
+  };
+
   const int steps = static_cast<int>(p.k / kBK);
   issue_loads(0, 0);
   __builtin_amdgcn_s_waitcnt(0);
@@ -403,13 +420,36 @@ gemm8_fast_kernel(Args p) {
     // B fragment of n-block j: k rows kb0 + 0..KLEN-1 of columns wn+16j..+15
     auto b_tr8 = [&](int j, int krow) -> i32x2 {
       const int row = krow + tr_jj;
-      const int chunk = ((wn + 16 * j) >> 4) ^ (row & 7);
+      const int chunk = ((wn + 16 * j) >> 4) ^ b_swz(row);
       const uint8_t* addr = b_src + row * kFBRow + chunk * 16 + 8 * tr_h;
       return __builtin_amdgcn_ds_read_tr8_b64_v2i32(reinterpret_cast<lds_i32x2*>(
           reinterpret_cast<uintptr_t>(addr)));
     };
 
     if constexpr (kFp8) {
+      constexpr int fmt = (KIND == FP8_E5M2) ? 1 : 0;
+      // Explicit software pipeline over the step's 32 MFMAs t = 4*i + j (row
+      // block i, column block j):
+      //  * the A fragment and row scales of block i+1 are read before block
+      //    i's MFMAs are issued;
+      //  * partial t is promoted right after MFMA t+2 is issued, so the
+      //    promotion never waits on an MFMA result and only three partials
+      //    are live;
+      //  * the step's last two partials are promoted at the start of the
+      //    next step, under the latency of its B-fragment reads.
+      // sched_barrier pins this order against the scheduler's reordering.
+      // A fragment: the chunk swizzle of row wm + 16i + li is a_swz(li) for every i.
+      const uint8_t* pa0 = a_src + (wm + li) * kFARow;
+      const int ca0 = ((2 * lk) ^ a_swz(li)) * 16, ca1 = ((2 * lk + 1) ^ a_swz(li)) * 16;
+      const float* sa0 = &sAs[cur * kFBM + wm + 4 * lk];
+      uint4 xa[8][2];
+      f32x4 scl[8];
+      auto read_a = [&](int i) {
+        xa[i][0] = *reinterpret_cast<const uint4*>(pa0 + i * 16 * kFARow + ca0);
+        xa[i][1] = *reinterpret_cast<const uint4*>(pa0 + i * 16 * kFARow + ca1);
+        scl[i] = *reinterpret_cast<const f32x4*>(sa0 + 16 * i);
+      };
+      read_a(0);
       i32x8 fb[4];
       float bs[4];
 #pragma unroll
@@ -419,53 +459,45 @@ gemm8_fast_kernel(Args p) {
         fb[j] = i32x8{q0[0], q0[1], q1[0], q1[1], q2[0], q2[1], q3[0], q3[1]};
         bs[j] = sBs[cur * kFBN + wn + 16 * j + li];
       }
-      constexpr int fmt = (KIND == FP8_E5M2) ? 1 : 0;
-      // Software pipeline over the 8 row blocks: the A fragment of block i+1 is
-      // read from LDS while block i's MFMAs run, and block i-1 is promoted
-      // after block i's MFMAs are issued, so neither an LDS read nor a
-      // promotion waits on the instruction just before it.
-      f32x4 part[2][4];
-      f32x4 scl[2];
-      // A fragment: the chunk swizzle (row & 7) equals (li & 7) for every row block.
-      const uint8_t* pa0 = a_src + (wm + li) * kFARow;
-      const int ca0 = ((2 * lk) ^ (li & 7)) * 16, ca1 = ((2 * lk + 1) ^ (li & 7)) * 16;
-      uint4 xa0 = *reinterpret_cast<const uint4*>(pa0 + ca0);
-      uint4 xa1 = *reinterpret_cast<const uint4*>(pa0 + ca1);
+      if (s > 0) {
+        promote16(acc_o[7][2], plast[0], UNIFORM_BS ? sclast : sclast * bslast[2]);
+        promote16(acc_o[7][3], plast[1], UNIFORM_BS ? sclast : sclast * bslast[3]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      f32x4 part[32];
+      f32x4 sc[8];  // uniform b_scale: block scale; else the row scales
 #pragma unroll
-      for (int i = 0; i <= 8; ++i) {
-        if (i < 8) {
-          const i32x8 fa = i32x8{(int)xa0.x, (int)xa0.y, (int)xa0.z, (int)xa0.w,
-                                 (int)xa1.x, (int)xa1.y, (int)xa1.z, (int)xa1.w};
-          scl[i & 1] = *reinterpret_cast<const f32x4*>(&sAs[cur * kFBM + wm + 16 * i + 4 * lk]);
+      for (int i = 0; i < 8; ++i) {
+        if (i + 1 < 8) read_a(i + 1);
+        const i32x8 fa = i32x8{(int)xa[i][0].x, (int)xa[i][0].y, (int)xa[i][0].z, (int)xa[i][0].w,
+                               (int)xa[i][1].x, (int)xa[i][1].y, (int)xa[i][1].z, (int)xa[i][1].w};
+        sc[i] = UNIFORM_BS ? scl[i] * bs[0] : scl[i];
 #pragma unroll
-          for (int j = 0; j < 4; ++j)
-            part[i & 1][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                fa, fb[j], f32x4{0.f, 0.f, 0.f, 0.f}, fmt, fmt, 0, 127, 0, 127);
-          if (i + 1 < 8) {
-            const uint8_t* pa = pa0 + (i + 1) * 16 * kFARow;
-            xa0 = *reinterpret_cast<const uint4*>(pa + ca0);
-            xa1 = *reinterpret_cast<const uint4*>(pa + ca1);
+        for (int j = 0; j < 4; ++j) {
+          const int t = 4 * i + j;
+          part[t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+              fa, fb[j], f32x4{0.f, 0.f, 0.f, 0.f}, fmt, fmt, 0, 127, 0, 127);
+          __builtin_amdgcn_sched_barrier(0);
+          if (t >= 2) {
+            const int u = t - 2, ui = u / 4, uj = u % 4;
+            promote16(acc_o[ui][uj], part[u], UNIFORM_BS ? sc[ui] : sc[ui] * bs[uj]);
           }
-        }
-        if (i > 0) {
-          const int ip = i - 1, sp = ip & 1;
-          if constexpr (UNIFORM_BS) {  // block_n % 64 == 0: one b_scale per wave
-            const f32x4 sc = scl[sp] * bs[0];
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-              for (int r = 0; r < 4; ++r)
-                acc_o[ip][j][r] = fmaf(part[sp][j][r], sc[r], acc_o[ip][j][r]);
-          } else {
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-              for (int r = 0; r < 4; ++r)
-                acc_o[ip][j][r] = fmaf(part[sp][j][r], scl[sp][r] * bs[j], acc_o[ip][j][r]);
-          }
+          __builtin_amdgcn_sched_barrier(0);
         }
       }
+      plast[0] = part[30];
+      plast[1] = part[31];
+      sclast = sc[7];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bslast[j] = bs[j];
     } else {
+      // A fragments are read one row block ahead of their MFMAs (the 16-row
+      // fragment of row block i: row wm + 16i + li, swizzle a_swz(li)).
+      auto read_a8 = [&](int h, int i) {
+        const int row = wm + 16 * i + li;
+        return *reinterpret_cast<const uint4*>(a_src + row * kFARow + ((4 * h + lk) ^ a_swz(li)) * 16);
+      };
+      uint4 xa = read_a8(0, 0);
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         i32x4 fb[4];
@@ -476,10 +508,9 @@ gemm8_fast_kernel(Args p) {
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const int row = wm + 16 * i + li;
-          const uint4 x = *reinterpret_cast<const uint4*>(a_src + row * kFARow +
-                                                          ((4 * h + lk) ^ (row & 7)) * 16);
-          const i32x4 fa = i32x4{(int)x.x, (int)x.y, (int)x.z, (int)x.w};
+          const i32x4 fa = i32x4{(int)xa.x, (int)xa.y, (int)xa.z, (int)xa.w};
+          if (i + 1 < 8) xa = read_a8(h, i + 1);
+          else if (h == 0) xa = read_a8(1, 0);
 #pragma unroll
           for (int j = 0; j < 4; ++j)
             acc_i[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa, fb[j], acc_i[i][j], 0, 0, 0);
@@ -490,6 +521,11 @@ gemm8_fast_kernel(Args p) {
     // asm, so the compiler does not hold LDS reads of step s behind them).
     __builtin_amdgcn_s_waitcnt(0);
     barrier_no_wait();
+  }
+
+  if constexpr (kFp8) {
+    promote16(acc_o[7][2], plast[0], UNIFORM_BS ? sclast : sclast * bslast[2]);
+    promote16(acc_o[7][3], plast[1], UNIFORM_BS ? sclast : sclast * bslast[3]);
   }
 
   // ---- epilogue: lane holds rows wm+16i+4lk+r, column wn+16j+li ----
