@@ -195,6 +195,26 @@ def wl_fp8_gemm(torch, ks, H):
     return fn, 8, nbytes, 2.0 * m * n * k
 
 
+def wl_fp8_plain(torch, ks, H):
+    """ks_gemm_fp8: per-token x per-channel scaled fp8 GEMM at the config 3 shape."""
+    import oracle as O
+    m, n, k = 2048, 7168, 7168
+    rng = np.random.default_rng(9)
+    a8 = torch.from_numpy(O.fp8_encode(rng.standard_normal((m, k)).astype(np.float32) * 50)).cuda()
+    b8 = torch.from_numpy(O.fp8_encode(rng.standard_normal((k, n)).astype(np.float32) * 50)).cuda()
+    a_s = torch.from_numpy(rng.uniform(0.001, 0.01, m).astype(np.float32)).cuda()
+    b_s = torch.from_numpy(rng.uniform(0.001, 0.01, n).astype(np.float32)).cuda()
+    a8 = a8.view(torch.float8_e4m3fn)
+    b8 = b8.view(torch.float8_e4m3fn)
+    out = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+
+    def fn(i):
+        ks.gemm.gemm_fp8(out, a8, b8, a_s, b_s, m, n, k)
+
+    nbytes = m * k + k * n + m * n * 2 + (m + n) * 4
+    return fn, 8, nbytes, 2.0 * m * n * k
+
+
 def wl_w8a8(torch, ks, H):
     m = n = k = 4096
     rng = np.random.default_rng(8)
@@ -360,6 +380,9 @@ def main():
             fn, per, nb, fl = wl_fp8_gemm(torch, ks, H)
             ms2, c2 = T.run(fn, per, max(32, steps // 8), 8, min_per_graph=8)
             sec["fp8_blockwise_gemm_M2048_N7168_K7168"] = line("fp8 gemm", ms2, c2, nb, fl, "mfma", "fp8")
+            fn, per, nb, fl = wl_fp8_plain(torch, ks, H)
+            ms2, c2 = T.run(fn, per, max(32, steps // 8), 8, min_per_graph=8)
+            sec["fp8_per_token_gemm_M2048_N7168_K7168"] = line("fp8 gemm per-token", ms2, c2, nb, fl, "mfma", "fp8")
         if "quant" in only:
             fn, per, nb, fl = wl_quant_group(torch, ks, H, 16)
             ms2, c2 = T.run(fn, per, steps, 32)

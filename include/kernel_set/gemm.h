@@ -1,13 +1,13 @@
 /*
  * kernel-set (MI355X build) -- quantized GEMMs.
  *
- * The three entry points keep the exact prototypes of the reference ABI
+ * The four entry points keep the exact prototypes of the reference ABI
  * (include/kernel_set/gemm.h of cklxx/kernel-set) so existing bindings load
  * this library unchanged. All matrices are row-major and device resident;
  * every call only enqueues work on `stream` (NULL = null stream).
  *
  * Out of scope for this build (not exported): ks_gemm, ks_gemm_bias_act,
- * ks_gemm_batched, ks_gemm_fp8 (per-token), ks_gemm_nvfp4.
+ * ks_gemm_batched, ks_gemm_nvfp4.
  */
 #ifndef KERNEL_SET_GEMM_H_
 #define KERNEL_SET_GEMM_H_
@@ -39,6 +39,18 @@ KS_API ks_status_t ks_gemm_w4a16(void* c, const void* a, const void* b_packed,
                                  const void* bias, int64_t m, int64_t n,
                                  int64_t k, int group_size, ks_dtype_t dtype,
                                  ks_stream_t stream);
+
+/* Replaces reference gemm.h:60-77 (kernels/src/gemm/gemm_fp8.cu:206-290).
+ * fp8 A [M,K] x fp8 B [K,N] (both e4m3 or both e5m2, fp8_dtype), fp32
+ * accumulation over all of K, then C = (acc * a_s) * b_s with a_scale fp32 [M]
+ * (KS_QUANT_PER_TOKEN) or [1] (PER_TENSOR) and b_scale fp32 [N]
+ * (KS_QUANT_PER_CHANNEL) or [1] (PER_TENSOR). out_dtype f32/f16/bf16. */
+KS_API ks_status_t ks_gemm_fp8(void* out, const void* a_fp8, const void* b_fp8,
+                               const float* a_scale, const float* b_scale,
+                               int64_t m, int64_t n, int64_t k,
+                               ks_quant_mode_t a_mode, ks_quant_mode_t b_mode,
+                               ks_dtype_t fp8_dtype, ks_dtype_t out_dtype,
+                               ks_stream_t stream);
 
 /* Replaces reference gemm.h:79-98 (kernels/src/gemm/gemm_fp8_blockwise.cu:218-302).
  * fp8 A [M,K] x fp8 B [K,N] with a_scale fp32 [M, ceil(K/block_k)] and b_scale

@@ -34,7 +34,13 @@ constexpr int kThreads = 256;
 constexpr int kBM = 128, kBN = 128, kBK = 128;
 constexpr int kLdsStride = kBK + 16;  // bytes per LDS row (16 B pad vs bank conflicts)
 
-enum Kind { FP8_E4M3 = 0, FP8_E5M2 = 1, INT8 = 2, INT8_RAW = 3 };
+// FP8_*: blockwise-scaled (ks_gemm_fp8_blockwise); FP8P_*: plain fp32
+// accumulation over all of K with per-token/per-channel scales (ks_gemm_fp8).
+enum Kind { FP8_E4M3 = 0, FP8_E5M2 = 1, INT8 = 2, INT8_RAW = 3, FP8P_E4M3 = 4, FP8P_E5M2 = 5 };
+
+constexpr bool is_fp8_block(int kind) { return kind == FP8_E4M3 || kind == FP8_E5M2; }
+constexpr bool is_fp8_plain(int kind) { return kind == FP8P_E4M3 || kind == FP8P_E5M2; }
+constexpr int fp8_fmt(int kind) { return (kind == FP8_E5M2 || kind == FP8P_E5M2) ? 1 : 0; }
 
 // 4x4 byte transpose: in[r] holds bytes (r,0..3); out[c] holds bytes (0..3,c).
 __device__ inline void transpose4x4(const uint32_t in[4], uint32_t out[4]) {
@@ -160,7 +166,11 @@ gemm8_kernel(Args p) {
     }
   };
 
-  constexpr bool kFp8 = (KIND == FP8_E4M3 || KIND == FP8_E5M2);
+  // Plain fp8 runs the blockwise path as one K block with unit scales (the
+  // promotion is then fma(P, 1, 0) = P exactly) and the per-token /
+  // per-channel epilogue of W8A8.
+  constexpr bool kPlain = is_fp8_plain(KIND);
+  constexpr bool kFp8 = is_fp8_block(KIND) || kPlain;
   // accumulators: 4x4 blocks of 16x16, 4 values per lane each
   f32x4 acc_o[4][4];   // fp8: promoted output; unused for int8
   f32x4 acc_p[4][4];   // fp8: raw partial of the current scale block
@@ -177,7 +187,7 @@ gemm8_kernel(Args p) {
   const int li = lane % 16;       // row (A) / column (B) inside a 16-block
   const int lk = lane / 16;       // k sub-slice
   const int steps = static_cast<int>((p.k + kBK - 1) / kBK);
-  const int steps_per_block = kFp8 ? p.block_k / kBK : 1;
+  const int steps_per_block = kPlain ? steps : (kFp8 ? p.block_k / kBK : 1);
 
   load_tiles(0);
   for (int s = 0; s < steps; ++s) {
@@ -186,13 +196,17 @@ gemm8_kernel(Args p) {
     store_tiles();
     const bool promote = kFp8 && ((s + 1) % steps_per_block == 0 || s + 1 == steps);
     if (kFp8 && promote) {
-      const int64_t kb = k0 / p.block_k;
-      if (t < kBM) {
-        const int64_t gm = m0 + t;
-        sAs[t] = gm < p.m ? p.a_scale[gm * p.nkb + kb] : 0.f;
+      if (kPlain) {
+        if (t < kBM) sAs[t] = 1.f; else sBs[t - kBM] = 1.f;
       } else {
-        const int64_t gn = n0 + (t - kBM);
-        sBs[t - kBM] = gn < p.n ? p.b_scale[kb * p.nnb + gn / p.block_n] : 0.f;
+        const int64_t kb = k0 / p.block_k;
+        if (t < kBM) {
+          const int64_t gm = m0 + t;
+          sAs[t] = gm < p.m ? p.a_scale[gm * p.nkb + kb] : 0.f;
+        } else {
+          const int64_t gn = n0 + (t - kBM);
+          sBs[t - kBM] = gn < p.n ? p.b_scale[kb * p.nnb + gn / p.block_n] : 0.f;
+        }
       }
     }
     __syncthreads();
@@ -213,7 +227,7 @@ gemm8_kernel(Args p) {
         fb[i] = i32x8{(int)y0.x, (int)y0.y, (int)y0.z, (int)y0.w,
                       (int)y1.x, (int)y1.y, (int)y1.z, (int)y1.w};
       }
-      constexpr int fmt = (KIND == FP8_E5M2) ? 1 : 0;  // 0 = fp8 e4m3, 1 = bf8 e5m2
+      constexpr int fmt = fp8_fmt(KIND);  // 0 = fp8 e4m3, 1 = bf8 e5m2
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -269,7 +283,12 @@ gemm8_kernel(Args p) {
       for (int r = 0; r < 4; ++r) {
         const int64_t gm = m0 + wm + 16 * i + 4 * lk + r;
         if (gm >= p.m) continue;
-        if constexpr (kFp8) {
+        if constexpr (kPlain) {
+          const float as = p.a_per_token ? p.a_scale[gm] : p.a_scale[0];
+          const float bs = p.b_per_channel ? p.b_scale[gn] : p.b_scale[0];
+          store_out<Out>(static_cast<typename Out::storage*>(p.out) + gm * p.n + gn,
+                         __fmul_rn(__fmul_rn(acc_o[i][j][r], as), bs));
+        } else if constexpr (kFp8) {
           store_out<Out>(static_cast<typename Out::storage*>(p.out) + gm * p.n + gn,
                          acc_o[i][j][r]);
         } else if constexpr (KIND == INT8_RAW) {
@@ -346,7 +365,8 @@ gemm8_fast_kernel(Args p) {
   const int wm = (wave / 4) * 128;
   const int wn = (wave % 4) * 64;
   const int li = lane % 16, lk = lane / 16;
-  constexpr bool kFp8 = (KIND == FP8_E4M3 || KIND == FP8_E5M2);
+  constexpr bool kFp8 = is_fp8_block(KIND);
+  constexpr bool kPlain = is_fp8_plain(KIND);
 
   // ---- per-lane global offsets of the direct-to-LDS loads (32-bit, checked
   // on the host). A: wave instruction i fills rows 8*(4*wave+i)..+7.
@@ -427,7 +447,7 @@ gemm8_fast_kernel(Args p) {
     };
 
     if constexpr (kFp8) {
-      constexpr int fmt = (KIND == FP8_E5M2) ? 1 : 0;
+      constexpr int fmt = fp8_fmt(KIND);
       // Explicit software pipeline over the step's 32 MFMAs t = 4*i + j (row
       // block i, column block j):
       //  * the A fragment and row scales of block i+1 are read before block
@@ -490,6 +510,34 @@ gemm8_fast_kernel(Args p) {
       sclast = sc[7];
 #pragma unroll
       for (int j = 0; j < 4; ++j) bslast[j] = bs[j];
+    } else if constexpr (kPlain) {
+      // Plain fp8: fp32 accumulation over all of K in the MFMA accumulator;
+      // A fragments are read one row block ahead of their MFMAs.
+      constexpr int fmt = fp8_fmt(KIND);
+      const uint8_t* pa0 = a_src + (wm + li) * kFARow;
+      const int ca0 = ((2 * lk) ^ a_swz(li)) * 16, ca1 = ((2 * lk + 1) ^ a_swz(li)) * 16;
+      uint4 xa0 = *reinterpret_cast<const uint4*>(pa0 + ca0);
+      uint4 xa1 = *reinterpret_cast<const uint4*>(pa0 + ca1);
+      i32x8 fbp[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const i32x2 q0 = b_tr8(j, 32 * lk + 0), q1 = b_tr8(j, 32 * lk + 8);
+        const i32x2 q2 = b_tr8(j, 32 * lk + 16), q3 = b_tr8(j, 32 * lk + 24);
+        fbp[j] = i32x8{q0[0], q0[1], q1[0], q1[1], q2[0], q2[1], q3[0], q3[1]};
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const i32x8 fa = i32x8{(int)xa0.x, (int)xa0.y, (int)xa0.z, (int)xa0.w,
+                               (int)xa1.x, (int)xa1.y, (int)xa1.z, (int)xa1.w};
+        if (i + 1 < 8) {
+          xa0 = *reinterpret_cast<const uint4*>(pa0 + (i + 1) * 16 * kFARow + ca0);
+          xa1 = *reinterpret_cast<const uint4*>(pa0 + (i + 1) * 16 * kFARow + ca1);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc_o[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+              fa, fbp[j], acc_o[i][j], fmt, fmt, 0, 127, 0, 127);
+      }
     } else {
       // A fragments are read one row block ahead of their MFMAs (the 16-row
       // fragment of row block i: row wm + 16i + li, swizzle a_swz(li)).
@@ -533,14 +581,18 @@ gemm8_fast_kernel(Args p) {
   for (int j = 0; j < 4; ++j) {
     const int64_t gn = n0 + wn + 16 * j + li;
     float bsc = 0.f;
-    if constexpr (KIND == INT8) bsc = p.b_per_channel ? p.b_scale[gn] : p.b_scale[0];
+    if constexpr (KIND == INT8 || kPlain) bsc = p.b_per_channel ? p.b_scale[gn] : p.b_scale[0];
 #pragma unroll
     for (int i = 0; i < 8; ++i)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int64_t gm = m0 + wm + 16 * i + 4 * lk + r;
         if (gm >= p.m) continue;
-        if constexpr (kFp8) {
+        if constexpr (kPlain) {
+          const float as = p.a_per_token ? p.a_scale[gm] : p.a_scale[0];
+          store_out<Out>(static_cast<typename Out::storage*>(p.out) + gm * p.n + gn,
+                         __fmul_rn(__fmul_rn(acc_o[i][j][r], as), bsc));
+        } else if constexpr (kFp8) {
           store_out<Out>(static_cast<typename Out::storage*>(p.out) + gm * p.n + gn, acc_o[i][j][r]);
         } else if constexpr (KIND == INT8_RAW) {
           static_cast<int32_t*>(p.out)[gm * p.n + gn] = acc_i[i][j][r];
@@ -574,6 +626,22 @@ fp8_blockwise_simple_kernel(Args p) {
     out = fmaf(part, p.a_scale[gm * p.nkb + kb] * p.b_scale[kb * p.nnb + gn / p.block_n], out);
   }
   store_out<Out>(static_cast<typename Out::storage*>(p.out) + idx, out);
+}
+
+// Any-shape plain fp8 fallback: k-ascending fp32 fma, then (acc * a_s) * b_s
+// (gemm_fp8.cu:120-157 order).
+template <typename Dec, typename Out>
+__global__ void __launch_bounds__(kThreads)
+fp8_plain_simple_kernel(Args p) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (idx >= p.m * p.n) return;
+  const int64_t gm = idx / p.n, gn = idx % p.n;
+  float acc = 0.f;
+  for (int64_t kk = 0; kk < p.k; ++kk)
+    acc = fmaf(Dec::dec(p.a[gm * p.k + kk]), Dec::dec(p.b[kk * p.n + gn]), acc);
+  const float as = p.a_per_token ? p.a_scale[gm] : p.a_scale[0];
+  const float bs = p.b_per_channel ? p.b_scale[gn] : p.b_scale[0];
+  store_out<Out>(static_cast<typename Out::storage*>(p.out) + idx, __fmul_rn(__fmul_rn(acc, as), bs));
 }
 
 // Any-shape W8A8 fallback.
@@ -662,6 +730,21 @@ void run_fp8(const Args& p, ks_dtype_t fp8, hipStream_t s) {
   }
 }
 
+template <typename Out>
+void run_fp8_plain(const Args& p, ks_dtype_t fp8, hipStream_t s) {
+  const bool tiled = tiled_ok(p);
+  const bool fast = tiled && fast_ok(p);
+  if (fp8 == KS_DTYPE_F8E4M3) {
+    if (fast) launch_fast<FP8P_E4M3, Out>(p, s);
+    else if (tiled) launch_tiled<FP8P_E4M3, Out>(p, s);
+    else hipLaunchKernelGGL((fp8_plain_simple_kernel<e4m3_t, Out>), dim3(simple_grid(p)), dim3(kThreads), 0, s, p);
+  } else {
+    if (fast) launch_fast<FP8P_E5M2, Out>(p, s);
+    else if (tiled) launch_tiled<FP8P_E5M2, Out>(p, s);
+    else hipLaunchKernelGGL((fp8_plain_simple_kernel<e5m2_t, Out>), dim3(simple_grid(p)), dim3(kThreads), 0, s, p);
+  }
+}
+
 template <int KIND, typename Out>
 void run_w8a8(const Args& p, hipStream_t s) {
   if (tiled_ok(p) && fast_ok(p)) launch_fast<KIND, Out>(p, s);
@@ -721,6 +804,47 @@ ks_status_t ks_gemm_fp8_blockwise(void* out, const void* a_fp8, const void* b_fp
     default: run_fp8<bf16_t>(p, fp8_dtype, s); break;
   }
   KS_LAUNCH_STATUS("ks_gemm_fp8_blockwise");
+  return KS_SUCCESS;
+}
+
+ks_status_t ks_gemm_fp8(void* out, const void* a_fp8, const void* b_fp8, const float* a_scale,
+                        const float* b_scale, int64_t m, int64_t n, int64_t k,
+                        ks_quant_mode_t a_mode, ks_quant_mode_t b_mode, ks_dtype_t fp8_dtype,
+                        ks_dtype_t out_dtype, ks_stream_t stream) {
+  KS_REQUIRE_PTR(out);
+  KS_REQUIRE_PTR(a_fp8);
+  KS_REQUIRE_PTR(b_fp8);
+  KS_REQUIRE_PTR(a_scale);
+  KS_REQUIRE_PTR(b_scale);
+  if (m <= 0 || n <= 0 || k <= 0) KS_FAIL(KS_ERROR_INVALID_ARGUMENT, "ks_gemm_fp8: bad shape");
+  if (mul_overflows(m, k) || mul_overflows(k, n) || mul_overflows(m, n))
+    KS_FAIL(KS_ERROR_UNSUPPORTED_SHAPE, "ks_gemm_fp8: M*K / K*N / M*N exceeds int64 range");
+  if (m * n / kThreads >= kMaxTiles)
+    KS_FAIL(KS_ERROR_UNSUPPORTED_SHAPE, "ks_gemm_fp8: tile grid exceeds grid limits");
+  if (a_mode != KS_QUANT_PER_TENSOR && a_mode != KS_QUANT_PER_TOKEN)
+    KS_FAIL(KS_ERROR_INVALID_ARGUMENT, "ks_gemm_fp8: a_mode must be per-tensor or per-token");
+  if (b_mode != KS_QUANT_PER_TENSOR && b_mode != KS_QUANT_PER_CHANNEL)
+    KS_FAIL(KS_ERROR_INVALID_ARGUMENT, "ks_gemm_fp8: b_mode must be per-tensor or per-channel");
+  if (fp8_dtype != KS_DTYPE_F8E4M3 && fp8_dtype != KS_DTYPE_F8E5M2)
+    KS_FAIL(KS_ERROR_UNSUPPORTED_DTYPE, "ks_gemm_fp8: fp8_dtype must be e4m3 or e5m2");
+  if (out_dtype != KS_DTYPE_F32 && out_dtype != KS_DTYPE_F16 && out_dtype != KS_DTYPE_BF16)
+    KS_FAIL(KS_ERROR_UNSUPPORTED_DTYPE, "ks_gemm_fp8: out_dtype must be f32/f16/bf16");
+  Args p{};
+  p.out = out;
+  p.a = static_cast<const uint8_t*>(a_fp8);
+  p.b = static_cast<const uint8_t*>(b_fp8);
+  p.a_scale = a_scale;
+  p.b_scale = b_scale;
+  p.m = m; p.n = n; p.k = k;
+  p.a_per_token = a_mode == KS_QUANT_PER_TOKEN;
+  p.b_per_channel = b_mode == KS_QUANT_PER_CHANNEL;
+  auto s = to_stream(stream);
+  switch (out_dtype) {
+    case KS_DTYPE_F32: run_fp8_plain<f32_t>(p, fp8_dtype, s); break;
+    case KS_DTYPE_F16: run_fp8_plain<f16_t>(p, fp8_dtype, s); break;
+    default: run_fp8_plain<bf16_t>(p, fp8_dtype, s); break;
+  }
+  KS_LAUNCH_STATUS("ks_gemm_fp8");
   return KS_SUCCESS;
 }
 

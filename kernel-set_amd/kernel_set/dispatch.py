@@ -1,7 +1,7 @@
 """``ks.dispatch`` entry points for the quantized-inference ops.
 
 Signatures follow the reference's ``bindings/python/kernel_set/dispatch.py``
-(``int8_gemm`` :327-331, ``w4a16`` :334-337, ``fp8_gemm_blockwise`` :377-384,
+(``fp8_gemm`` :321-324, ``int8_gemm`` :327-331, ``w4a16`` :334-337, ``fp8_gemm_blockwise`` :377-384,
 ``per_token_group_quant`` :387-391, ``moe`` :539-543) and the output allocation
 of its kernel-set adapters (``backends/_registry.py:464-492,723-731,1204-1218``).
 There is exactly one provider, the native gfx950 library: no routing, no
@@ -19,7 +19,7 @@ from ._tensor import dtype_to_ks
 from .enums import DType
 
 PROVIDER = "kernel-set"
-_OPS = ("w4a16", "int8_gemm", "fp8_gemm_blockwise", "per_token_group_quant", "moe")
+_OPS = ("w4a16", "int8_gemm", "fp8_gemm", "fp8_gemm_blockwise", "per_token_group_quant", "moe")
 
 __all__ = list(_OPS) + ["which", "available", "providers", "chain", "ops"]
 
@@ -49,6 +49,28 @@ def int8_gemm(a8, b8, a_scale, b_scale, *, out_dtype=None, **kw):
         b_mode = QuantMode.PER_CHANNEL
     _gemm.gemm_w8a8(out, a8, b8, a_scale, b_scale, m=m, n=n, k=k, bias=kw.get("bias"),
                     a_mode=a_mode, b_mode=b_mode, out_dtype=dtype_to_ks(out.dtype))
+    return out
+
+
+def fp8_gemm(a8, b8, a_scale, b_scale, *, out_dtype=None, **kw):
+    """Scaled fp8 GEMM ``C = (a_scale (x) b_scale) * (a8 @ b8.T)``. ``b8`` is
+    ``[N, K]`` (the NT weight layout of the reference's fp8_gemm providers,
+    ``backends/_registry.py:427-442``); ``a_scale`` is ``[M]``/``[M,1]`` or one
+    element, ``b_scale`` ``[N]``/``[1,N]`` or one element; default bf16 out.
+    ``ks_gemm_fp8`` takes B as ``[K, N]``, so ``b8`` is transposed once here."""
+    m, k = a8.shape
+    n = b8.shape[0]
+    out = torch.empty(m, n, device=a8.device, dtype=out_dtype or torch.bfloat16)
+    from .enums import QuantMode
+    a_mode = QuantMode.PER_TENSOR if a_scale.numel() == 1 else QuantMode.PER_TOKEN
+    b_mode = QuantMode.PER_TENSOR if b_scale.numel() == 1 else QuantMode.PER_CHANNEL
+    if a_mode == QuantMode.PER_TOKEN and a_scale.numel() != m:
+        raise ValueError(f"fp8_gemm: a_scale must have 1 or M={m} elements")
+    if b_mode == QuantMode.PER_CHANNEL and b_scale.numel() != n:
+        raise ValueError(f"fp8_gemm: b_scale must have 1 or N={n} elements")
+    b_kn = b8.t().contiguous()
+    _gemm.gemm_fp8(out, a8, b_kn, a_scale.contiguous(), b_scale.contiguous(), m=m, n=n, k=k,
+                   a_mode=a_mode, b_mode=b_mode, out_dtype=dtype_to_ks(out.dtype))
     return out
 
 

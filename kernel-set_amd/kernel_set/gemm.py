@@ -1,7 +1,7 @@
 """Quantized GEMMs (``include/kernel_set/gemm.h``).
 
 Same function names, argument order and defaults as the reference's
-``bindings/python/kernel_set/gemm.py:151-362`` for the three quantized GEMMs.
+``bindings/python/kernel_set/gemm.py:151-362`` for the four quantized GEMMs.
 """
 from __future__ import annotations
 
@@ -12,7 +12,7 @@ from ._lib import check, lib
 from ._tensor import TensorLike, _is_tensor, default_stream, dtype_to_ks, infer_dtype, ptr
 from .enums import QuantMode
 
-__all__ = ["gemm_w8a8", "gemm_w4a16", "gemm_fp8_blockwise"]
+__all__ = ["gemm_w8a8", "gemm_w4a16", "gemm_fp8", "gemm_fp8_blockwise"]
 
 _F32P = POINTER(c_float)
 
@@ -58,6 +58,24 @@ def gemm_w4a16(c: TensorLike, a: TensorLike, b_packed: TensorLike, scales: Tenso
         int(m), int(n), int(k), int(group_size), dt, default_stream(stream, a)),
         "ks_gemm_w4a16")
     return c
+
+
+def gemm_fp8(out: TensorLike, a_fp8: TensorLike, b_fp8: TensorLike, a_scale: TensorLike,
+             b_scale: TensorLike, m: int, n: int, k: int,
+             a_mode: int = QuantMode.PER_TOKEN, b_mode: int = QuantMode.PER_CHANNEL,
+             fp8_dtype: int = None, out_dtype: int = None,
+             stream: TensorLike = None) -> TensorLike:
+    """fp8 ``A [M,K]`` x fp8 ``B [K,N]`` -> ``C [M,N]`` in ``out_dtype``: fp32
+    accumulation, then ``(acc * a_scale) * b_scale`` (reference gemm.py:228-280).
+    ``fp8_dtype`` is inferred from ``a_fp8`` and ``out_dtype`` from ``out``."""
+    fdt = infer_dtype(a_fp8, fp8_dtype)
+    odt = _out_dtype(out, out_dtype, "ks_gemm_fp8")
+    check(lib.ks_gemm_fp8(
+        ptr(out, name="out"), ptr(a_fp8, name="a_fp8"), ptr(b_fp8, name="b_fp8"),
+        _f32(a_scale, name="a_scale"), _f32(b_scale, name="b_scale"),
+        int(m), int(n), int(k), int(a_mode), int(b_mode), fdt, odt,
+        default_stream(stream, out if not isinstance(out, int) else a_fp8)), "ks_gemm_fp8")
+    return out
 
 
 def gemm_fp8_blockwise(out: TensorLike, a_fp8: TensorLike, b_fp8: TensorLike,

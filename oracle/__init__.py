@@ -51,6 +51,7 @@ def lib() -> ctypes.CDLL:
             "oracle_dequant_int4": [P, P, P, P, I64, I64, I64],
             "oracle_w4a16": [P, P, P, P, P, P, I64, I64, I64, I64],
             "oracle_fp8_blockwise": [P, P, P, P, P, I64, I64, I64, I64, I64, I],
+            "oracle_fp8_gemm": [P, P, P, P, P, I64, I64, I64, I, I, I],
             "oracle_w8a8_acc": [P, P, P, I64, I64, I64],
             "oracle_w8a8_epilogue": [P, P, P, P, P, I64, I64, I, I],
         }
@@ -282,6 +283,35 @@ def fp8_blockwise_ref(a8, b8, a_scale, b_scale, block_n=128, block_k=128, fmt=E4
     """bench.py:1502: a_deq @ b_deq in fp32."""
     a_deq, b_deq = fp8_blockwise_dequant(a8, b8, a_scale, b_scale, block_n, block_k, fmt)
     return (a_deq @ b_deq).astype(np.float32)
+
+
+def fp8_gemm_scalar(a8, b8, a_scale, b_scale, a_per_token=True, b_per_channel=True,
+                    fmt=E4M3) -> np.ndarray:
+    """gemm_fp8.cu:98-157 in the reference's operation order (scalar C)."""
+    a8 = _c(a8, np.uint8)
+    b8 = _c(b8, np.uint8)
+    m, k = a8.shape
+    n = b8.shape[1]
+    out = np.empty((m, n), np.float32)
+    lib().oracle_fp8_gemm(_p(a8), _p(b8), _p(_c(a_scale, np.float32)),
+                          _p(_c(b_scale, np.float32)), _p(out), m, n, k,
+                          int(a_per_token), int(b_per_channel), fmt)
+    return out
+
+
+def fp8_gemm_ref(a8, b8, a_scale, b_scale, a_per_token=True, b_per_channel=True,
+                 fmt=E4M3) -> np.ndarray:
+    """gemm.h:60-70 closed form C = (a_scale (x) b_scale) * (A_fp8 @ B_fp8):
+    decode both operands exactly, fp32 matmul, then scale."""
+    a = fp8_decode(a8, fmt).astype(np.float32)
+    b = fp8_decode(b8, fmt).astype(np.float32)
+    acc = (a @ b).astype(np.float32)
+    m, n = acc.shape
+    asv = _c(a_scale, np.float32).reshape(-1)
+    bsv = _c(b_scale, np.float32).reshape(-1)
+    col_a = asv[:m].reshape(m, 1) if a_per_token else asv[0]
+    row_b = bsv[:n].reshape(1, n) if b_per_channel else bsv[0]
+    return ((acc * col_a).astype(np.float32) * row_b).astype(np.float32)
 
 
 def w8a8_acc(a_i8, b_i8) -> np.ndarray:

@@ -205,6 +205,22 @@ void oracle_fp8_blockwise(const uint8_t* a, const uint8_t* b, const float* as,
     }
 }
 
+/* gemm_fp8.cu:98-157: fp32 accumulation over all of K in ascending k (the
+ * reference's acc += a*b, contracted to an fma), then (acc * a_s) * b_s. */
+void oracle_fp8_gemm(const uint8_t* a, const uint8_t* b, const float* as,
+                     const float* bs, float* c, int64_t m, int64_t n, int64_t k,
+                     int a_per_token, int b_per_channel, int fmt) {
+  for (int64_t i = 0; i < m; ++i)
+    for (int64_t j = 0; j < n; ++j) {
+      float acc = 0.0f;
+      for (int64_t kk = 0; kk < k; ++kk)
+        acc = fmaf(fp8_decode(a[i * k + kk], fmt), fp8_decode(b[kk * n + j], fmt), acc);
+      float v = acc * (a_per_token ? as[i] : as[0]);
+      v = v * (b_per_channel ? bs[j] : bs[0]);
+      c[i * n + j] = v;
+    }
+}
+
 /* gemm_w8a8.cu:120-142: exact int32 accumulation. */
 void oracle_w8a8_acc(const int8_t* a, const int8_t* b, int32_t* acc, int64_t m,
                      int64_t n, int64_t k) {

@@ -104,6 +104,26 @@ def test_w8a8_validation():
     assert f(P, P, P, fp, fp, None, 1, -1, 1, 1, 2, DType.BF16, None) == Status.ERROR_INVALID_ARGUMENT
 
 
+def test_fp8_gemm_validation():
+    # gemm_fp8.cu:230-275 order: NULL pointers, shape, overflow, modes, dtypes
+    f = _lib.lib.ks_gemm_fp8
+    fp = ctypes.cast(P, _lib._F32P)
+    ok = (QuantMode.PER_TOKEN, QuantMode.PER_CHANNEL, DType.F8E4M3, DType.BF16, None)
+    assert f(P, P, P, fp, None, 1, 1, 1, *ok) == Status.ERROR_INVALID_ARGUMENT
+    assert ks.last_error_string() == "null arg: b_scale"
+    assert f(P, P, P, fp, fp, 0, 1, 1, *ok) == Status.ERROR_INVALID_ARGUMENT
+    big = 1 << 40
+    assert f(P, P, P, fp, fp, big, big, 8, *ok) == Status.ERROR_UNSUPPORTED_SHAPE
+    assert f(P, P, P, fp, fp, 1, 1, 1, QuantMode.PER_CHANNEL, QuantMode.PER_CHANNEL,
+             DType.F8E4M3, DType.BF16, None) == Status.ERROR_INVALID_ARGUMENT
+    assert f(P, P, P, fp, fp, 1, 1, 1, QuantMode.PER_TOKEN, QuantMode.PER_TOKEN,
+             DType.F8E4M3, DType.BF16, None) == Status.ERROR_INVALID_ARGUMENT
+    assert f(P, P, P, fp, fp, 1, 1, 1, QuantMode.PER_TOKEN, QuantMode.PER_CHANNEL,
+             DType.I8, DType.BF16, None) == Status.ERROR_UNSUPPORTED_DTYPE
+    assert f(P, P, P, fp, fp, 1, 1, 1, QuantMode.PER_TOKEN, QuantMode.PER_CHANNEL,
+             DType.F8E5M2, DType.I8, None) == Status.ERROR_UNSUPPORTED_DTYPE
+
+
 def test_fp8_blockwise_validation():
     f = _lib.lib.ks_gemm_fp8_blockwise
     fp = ctypes.cast(P, _lib._F32P)
@@ -166,7 +186,7 @@ def test_python_wrappers_raise_kernel_set_error():
 
 def test_dispatch_introspection():
     d = ks.dispatch
-    assert set(d.ops()) == {"w4a16", "int8_gemm", "fp8_gemm_blockwise",
+    assert set(d.ops()) == {"w4a16", "int8_gemm", "fp8_gemm", "fp8_gemm_blockwise",
                             "per_token_group_quant", "moe"}
     for op in d.ops():
         assert d.which(op) == "kernel-set" and d.chain(op) == ["kernel-set"]

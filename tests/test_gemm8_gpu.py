@@ -1,4 +1,10 @@
-"""GPU parity: fp8 blockwise GEMM and W8A8 int8 GEMM against the oracle.
+"""GPU parity: fp8 blockwise GEMM, plain scaled fp8 GEMM and W8A8 int8 GEMM
+against the oracle.
+
+fp8 (ks_gemm_fp8): max |out - ref| / max |ref| <= 1e-2 against the closed form
+(a_s (x) b_s) * (A @ B) with exactly decoded operands; exact for integer-valued
+operands with unit scales; the any-shape fallback is bit-exact against the
+scalar oracle (same k order, same (acc * a_s) * b_s epilogue).
 
 fp8 blockwise: max |out - ref| / max |ref| <= 1e-2 against the fp32
 dequantize-then-matmul reference (north_star; bench.py:1434-1502 restated);
@@ -98,6 +104,86 @@ def test_fp8_blockwise_integer_exact():
     b_s = np.ones((k // 128, n // 128 + 1), np.float32)
     got = run_fp8(O.fp8_encode(ai), O.fp8_encode(bi), a_s, b_s, 128, 128, out="f32")
     assert np.array_equal(got, (ai.astype(np.int64) @ bi.astype(np.int64)).astype(np.float32))
+
+
+def run_fp8_plain(a8, b8, a_s, b_s, per_tok=True, per_ch=True, fmt=O.E4M3, out="bf16"):
+    m, k = a8.shape
+    n = b8.shape[1]
+    fdt, tdt = FP8[fmt]
+    o = torch.empty(m, n, device="cuda", dtype=H.torch_dtype(out))
+    ks.gemm.gemm_fp8(o, H.np_u8_dev(a8).view(tdt), H.np_u8_dev(b8).view(tdt),
+                     H.np_f32_dev(a_s), H.np_f32_dev(b_s), m, n, k,
+                     a_mode=QuantMode.PER_TOKEN if per_tok else QuantMode.PER_TENSOR,
+                     b_mode=QuantMode.PER_CHANNEL if per_ch else QuantMode.PER_TENSOR,
+                     fp8_dtype=fdt)
+    torch.cuda.synchronize()
+    return H.from_dev_f32(o)
+
+
+def fp8_plain_case(m, n, k, fmt=O.E4M3, seed=0):
+    """Per-token activations and per-channel weights, both quantized the
+    reference way (amax / qmax per row / per output column)."""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    a8, a_s = O.quant_row(O.round_bf16(x), fmt)
+    w = (rng.standard_normal((k, n)) * 0.02).astype(np.float32)
+    wt8, b_s = O.quant_row(w.T.copy(), fmt)
+    return a8, np.ascontiguousarray(wt8.T), a_s, b_s
+
+
+@pytest.mark.parametrize("m,n,k", [(256, 256, 128), (512, 768, 1024), (130, 208, 384),
+                                   (1, 64, 256), (77, 1040, 1056), (2048, 512, 7168)])
+@pytest.mark.parametrize("out", ["bf16", "f32"])
+def test_fp8_plain_shapes(m, n, k, out):
+    a8, b8, a_s, b_s = fp8_plain_case(m, n, k, seed=m + 3 * n + k)
+    got = run_fp8_plain(a8, b8, a_s, b_s, out=out)
+    assert O.rel_err(got, O.fp8_gemm_ref(a8, b8, a_s, b_s)) <= TOL
+
+
+@pytest.mark.parametrize("per_tok,per_ch", [(False, False), (True, False), (False, True)])
+def test_fp8_plain_scale_modes(per_tok, per_ch):
+    a8, b8, a_s, b_s = fp8_plain_case(256, 512, 512, seed=9)
+    sa = a_s if per_tok else a_s[:1].copy()
+    sb = b_s if per_ch else b_s[:1].copy()
+    got = run_fp8_plain(a8, b8, sa, sb, per_tok, per_ch)
+    assert O.rel_err(got, O.fp8_gemm_ref(a8, b8, sa, sb, per_tok, per_ch)) <= TOL
+
+
+def test_fp8_plain_e5m2():
+    a8, b8, a_s, b_s = fp8_plain_case(256, 256, 512, fmt=O.E5M2, seed=4)
+    got = run_fp8_plain(a8, b8, a_s, b_s, fmt=O.E5M2)
+    assert O.rel_err(got, O.fp8_gemm_ref(a8, b8, a_s, b_s, fmt=O.E5M2)) <= 2e-2
+
+
+def test_fp8_plain_integer_exact():
+    rng = np.random.default_rng(31)
+    for m, n, k in ((256, 256, 640), (160, 192, 640), (33, 40, 70)):  # fast, tiled, scalar
+        ai = rng.integers(-8, 9, (m, k)).astype(np.float32)
+        bi = rng.integers(-8, 9, (k, n)).astype(np.float32)
+        got = run_fp8_plain(O.fp8_encode(ai), O.fp8_encode(bi), np.ones(m, np.float32),
+                            np.ones(n, np.float32), out="f32")
+        assert np.array_equal(got, (ai.astype(np.int64) @ bi.astype(np.int64)).astype(np.float32))
+
+
+def test_fp8_plain_fallback_bitexact():
+    # K not a multiple of 16 -> the per-element kernel, which keeps the
+    # reference's k order and epilogue: bit-exact against the scalar oracle.
+    a8, b8, a_s, b_s = fp8_plain_case(19, 23, 45, seed=6)
+    got = run_fp8_plain(a8, b8, a_s, b_s, out="f32")
+    assert np.array_equal(got, O.fp8_gemm_scalar(a8, b8, a_s, b_s))
+
+
+def test_fp8_gemm_dispatch_nt_layout():
+    # ks.dispatch.fp8_gemm takes the weight as [N, K] (the reference's NT
+    # provider layout) and a_scale/b_scale as torch._scaled_mm-style vectors.
+    a8, b8, a_s, b_s = fp8_plain_case(128, 256, 384, seed=8)
+    tdt = torch.float8_e4m3fn
+    out = ks.dispatch.fp8_gemm(H.np_u8_dev(a8).view(tdt),
+                               H.np_u8_dev(np.ascontiguousarray(b8.T)).view(tdt),
+                               H.np_f32_dev(a_s.reshape(-1, 1)), H.np_f32_dev(b_s.reshape(1, -1)))
+    torch.cuda.synchronize()
+    assert out.dtype == torch.bfloat16 and tuple(out.shape) == (128, 256)
+    assert O.rel_err(H.from_dev_f32(out), O.fp8_gemm_ref(a8, b8, a_s, b_s)) <= TOL
 
 
 def test_fp8_blockwise_fallback_golden_bitexact():

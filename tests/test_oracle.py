@@ -242,6 +242,43 @@ def test_fp8_blockwise_scalar_vs_dequant_reference():
     assert O.rel_err(f["c_f32"], bad) > 1e-2
 
 
+def test_fp8_gemm_integer_special_case_exact():
+    # gemm_fp8.cu with unit scales and integer-valued e4m3 operands is an exact
+    # integer matmul (every partial sum is an integer below 2^24).
+    rng = np.random.default_rng(21)
+    m, n, k = 6, 11, 90
+    a_int = rng.integers(-8, 9, (m, k)).astype(np.float32)
+    b_int = rng.integers(-8, 9, (k, n)).astype(np.float32)
+    a8, b8 = O.fp8_encode(a_int), O.fp8_encode(b_int)
+    exact = (a_int.astype(np.int64) @ b_int.astype(np.int64)).astype(np.float32)
+    for per_tok, per_ch in ((True, True), (False, False), (True, False)):
+        sa = np.ones(m if per_tok else 1, np.float32)
+        sb = np.ones(n if per_ch else 1, np.float32)
+        assert np.array_equal(O.fp8_gemm_scalar(a8, b8, sa, sb, per_tok, per_ch), exact)
+        assert np.array_equal(O.fp8_gemm_ref(a8, b8, sa, sb, per_tok, per_ch), exact)
+
+
+def test_fp8_gemm_scales_and_modes():
+    rng = np.random.default_rng(22)
+    m, n, k = 5, 7, 64
+    a8 = O.fp8_encode(rng.standard_normal((m, k)).astype(np.float32) * 4)
+    b8 = O.fp8_encode(rng.standard_normal((k, n)).astype(np.float32) * 4)
+    sa = rng.uniform(0.01, 0.1, m).astype(np.float32)
+    sb = rng.uniform(0.01, 0.1, n).astype(np.float32)
+    acc = O.fp8_gemm_scalar(a8, b8, np.ones(m, np.float32), np.ones(n, np.float32))
+    # (acc * a_s) * b_s, left to right in fp32 (gemm_fp8.cu:154)
+    exp = (acc * sa[:, None]).astype(np.float32) * sb[None, :]
+    assert np.array_equal(O.fp8_gemm_scalar(a8, b8, sa, sb), exp.astype(np.float32))
+    # per-tensor modes read element 0 only
+    pt = O.fp8_gemm_scalar(a8, b8, sa, sb, False, False)
+    assert np.array_equal(pt, ((acc * sa[0]).astype(np.float32) * sb[0]).astype(np.float32))
+    # closed form agrees with the scalar order to fp32 rounding; swapping the
+    # roles of the scales is caught
+    assert O.rel_err(O.fp8_gemm_scalar(a8, b8, sa, sb), O.fp8_gemm_ref(a8, b8, sa, sb)) < 1e-5
+    assert O.rel_err(O.fp8_gemm_scalar(a8, b8, sa, sb),
+                     O.fp8_gemm_ref(a8, b8, sa[::-1].copy(), sb, True, True)) > 1e-2
+
+
 def test_w8a8_accumulators_three_ways():
     rng = np.random.default_rng(14)
     a = rng.integers(-127, 128, (7, 50)).astype(np.int8)
