@@ -30,7 +30,7 @@ __device__ inline void load8(const typename T::storage* p, float v[8]);
 
 template <>
 __device__ inline void load8<bf16_t>(const uint16_t* p, float v[8]) {
-  const uint4 w = *reinterpret_cast<const uint4*>(p);
+  const uint4 w = load_stream16(p);
   const uint32_t d[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -41,7 +41,7 @@ __device__ inline void load8<bf16_t>(const uint16_t* p, float v[8]) {
 
 template <>
 __device__ inline void load8<f16_t>(const uint16_t* p, float v[8]) {
-  const uint4 w = *reinterpret_cast<const uint4*>(p);
+  const uint4 w = load_stream16(p);
   const uint32_t d[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -136,6 +136,7 @@ struct enc8<i8_t> {
 };
 
 constexpr int kGroupUnroll = 1;  // slots per thread (2 and 4 measured slower)
+constexpr unsigned kLoopBlocks = 2048;  // persistent grid of the per-block quantizer
 
 template <typename In, typename Enc, int LOG_L, typename Idx>
 __global__ void __launch_bounds__(kThreads)
@@ -159,24 +160,78 @@ group_quant_vec_kernel(uint8_t* __restrict__ out, float* __restrict__ scale,
     const Idx grp = live_slot ? slot - row * ngroups : 0;
     const Idx col = grp * group_size + static_cast<Idx>(sub) * 8;
     live[u] = live_slot && col < cols;
-    off[u] = row * cols + col;
+    off[u] = live[u] ? row * cols + col : 0;  // unconditional load (branch-free)
     sidx[u] = row * ngroups + grp;
     amax[u] = 0.f;
-    if (live[u]) load8<In>(in + off[u], v[u]);
+    load8<In>(in + off[u], v[u]);
   }
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    if (live[u]) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) amax[u] = fmaxf(amax[u], fabsf(v[u][i]));
-    }
+    for (int i = 0; i < 8; ++i) amax[u] = fmaxf(amax[u], live[u] ? fabsf(v[u][i]) : 0.f);
     amax[u] = group_max(amax[u], L);
     const float sc = scale_from_amax<Enc>(amax[u]);
     const float inv = 1.0f / sc;
     if (live[u]) {
-      *reinterpret_cast<uint2*>(out + off[u]) = enc8<Enc>::run(v[u], inv);
+      const uint2 code = enc8<Enc>::run(v[u], inv);
+      __builtin_nontemporal_store(code.x, reinterpret_cast<uint32_t*>(out + off[u]));
+      __builtin_nontemporal_store(code.y, reinterpret_cast<uint32_t*>(out + off[u]) + 1);
       if (sub == 0) scale[sidx[u]] = sc;
     }
+  }
+}
+
+// Persistent variant: a fixed grid walks the slots with stride gridDim *
+// kThreads, loading slot i+1 before it quantizes slot i.
+template <typename In, typename Enc, int LOG_L, typename Idx>
+__global__ void __launch_bounds__(kThreads)
+group_quant_loop_kernel(uint8_t* __restrict__ out, float* __restrict__ scale,
+                        const typename In::storage* __restrict__ in,
+                        Idx rows, Idx cols, Idx group_size, Idx ngroups) {
+  constexpr int L = 1 << LOG_L;
+  const int sub = static_cast<int>(threadIdx.x & (L - 1));
+  const Idx nthreads = rows * ngroups * L;
+  const Idx stride = static_cast<Idx>(gridDim.x) * kThreads;
+  Idx tid = static_cast<Idx>(blockIdx.x) * kThreads + threadIdx.x;
+  auto locate = [&](Idx t, Idx* off, Idx* sidx, bool* live) {
+    const Idx slot = t >> LOG_L;
+    const bool ls = t < nthreads;
+    const Idx row = ls ? slot / ngroups : 0;
+    const Idx grp = ls ? slot - row * ngroups : 0;
+    const Idx col = grp * group_size + static_cast<Idx>(sub) * 8;
+    *live = ls && col < cols;
+    *off = *live ? row * cols + col : 0;
+    *sidx = row * ngroups + grp;
+  };
+  Idx off, sidx;
+  bool live;
+  locate(tid, &off, &sidx, &live);
+  float v[8];
+  load8<In>(in + off, v);
+  // every lane of a wave runs the same number of rounds (uniform trip count)
+  const Idx wave0 = tid - (threadIdx.x & (kWave - 1));
+  for (Idx t0 = wave0; t0 < nthreads; t0 += stride) {
+    Idx noff, nsidx;
+    bool nlive;
+    locate(tid + stride, &noff, &nsidx, &nlive);
+    float nv[8];
+    load8<In>(in + noff, nv);
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, live ? fabsf(v[i]) : 0.f);
+    amax = group_max(amax, L);
+    const float sc = scale_from_amax<Enc>(amax);
+    const float inv = 1.0f / sc;
+    if (live) {
+      const uint2 code = enc8<Enc>::run(v, inv);
+      __builtin_nontemporal_store(code.x, reinterpret_cast<uint32_t*>(out + off));
+      __builtin_nontemporal_store(code.y, reinterpret_cast<uint32_t*>(out + off) + 1);
+      if (sub == 0) scale[sidx] = sc;
+    }
+    tid += stride;
+    off = noff; sidx = nsidx; live = nlive;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = nv[i];
   }
 }
 
@@ -439,10 +494,19 @@ void launch_group(uint8_t* out, float* scale, const void* input, int64_t rows,
     auto go = [&](auto log_tag, auto idx_tag) {
       constexpr int LL = decltype(log_tag)::value;
       using I = typename decltype(idx_tag)::type;
-      hipLaunchKernelGGL((group_quant_vec_kernel<In, Enc, LL, I>), dim3(static_cast<unsigned>(blocks)),
-                         dim3(kThreads), 0, s, out, scale, static_cast<const S*>(input),
-                         static_cast<I>(rows), static_cast<I>(cols), static_cast<I>(gs),
-                         static_cast<I>(ngroups));
+      // Large inputs: a persistent grid of kLoopBlocks workgroups (measured on
+      // MI355X at 2048x7168: 10.1 us against 10.6 us for one slot per thread;
+      // 512 or 1024 workgroups were slower).
+      if (blocks > kLoopBlocks)
+        hipLaunchKernelGGL((group_quant_loop_kernel<In, Enc, LL, I>), dim3(kLoopBlocks),
+                           dim3(kThreads), 0, s, out, scale, static_cast<const S*>(input),
+                           static_cast<I>(rows), static_cast<I>(cols), static_cast<I>(gs),
+                           static_cast<I>(ngroups));
+      else
+        hipLaunchKernelGGL((group_quant_vec_kernel<In, Enc, LL, I>),
+                           dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, s, out,
+                           scale, static_cast<const S*>(input), static_cast<I>(rows),
+                           static_cast<I>(cols), static_cast<I>(gs), static_cast<I>(ngroups));
     };
     auto by_idx = [&](auto log_tag) {
       if (small) go(log_tag, type_tag<uint32_t>{});

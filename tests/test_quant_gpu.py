@@ -49,6 +49,17 @@ def test_quantize_fp8_group_bitexact(dt, fmt, rows, cols, gs):
     assert np.array_equal(q, eq)
 
 
+@pytest.mark.parametrize("rows,cols,gs", [(1531, 7168, 128), (777, 4104, 64)])
+def test_quantize_fp8_group_persistent_grid_bitexact(rows, cols, gs):
+    # More than 2048 workgroups of slots: the persistent kernel, including a
+    # trip count that does not divide the grid and a ragged last group.
+    t, xv = _inputs(rows, cols, "bf16", seed=rows + cols)
+    q, s = _group(t, rows, cols, gs, O.E4M3, "bf16")
+    eq, es = O.quant_group(xv, gs, O.E4M3)
+    assert np.array_equal(s.view(np.uint32), es.view(np.uint32))
+    assert np.array_equal(q, eq)
+
+
 def test_quantize_fp8_group_golden():
     f = np.load(os.path.join(GOLDEN, "quant_fp8_group.npz"))
     t, _ = H.to_dev(f["x_bf16_vals"], "bf16")
