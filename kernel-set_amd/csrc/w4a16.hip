@@ -44,7 +44,8 @@ constexpr int kThreads = 256;
 constexpr int kLanesN = 8;                    // lanes across the column tile
 constexpr int kTileN = kLanesN * 16;          // 128 columns per workgroup
 constexpr int kRowsPar = kThreads / kLanesN;  // 32 row lanes
-constexpr int kMaxGemvM = 8;
+constexpr int kMaxGemvM = 8;   // dot2 decode kernel
+constexpr int kMaxDecM = 8;    // MFMA decode kernel (up to 2 blocks of 4 activation rows)
 constexpr int kDqMinM = 64;  // above this M the dequantize-to-LDS MFMA GEMM runs (measured crossover)
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -508,7 +509,7 @@ ks_status_t dec_rows(uint16_t* c, const uint16_t* a, const uint8_t* b, const uin
   const int splits = static_cast<int>((k / 2 + rows_wg - 1) / rows_wg);
   Scratch sc;
   if (splits > 1) {
-    ks_status_t r = get_scratch(st, static_cast<size_t>(splits) * kMaxGemvM * n, 0, &sc,
+    ks_status_t r = get_scratch(st, static_cast<size_t>(splits) * kMaxDecM * n, 0, &sc,
                                 "ks_gemm_w4a16");
     if (r != KS_SUCCESS) return r;
   }
@@ -562,6 +563,13 @@ ks_status_t run(void* c_, const void* a_, const void* b_, const void* s_, const 
   const bool pipe = m > kMaxGemvM && (gs % 64 == 0) && (k % w4pipe::kStageK == 0) && (n % 16 == 0) &&
                     aligned(a, 16) && aligned(b, 16) && aligned(s, 4) && aligned(z, 4) &&
                     k * n < (int64_t{1} << 40);
+  // M <= 8: the MFMA decode kernel (measured on MI355X at K=4096, N=14336:
+  // M=8 15.6 us against 33.3 us for the dot2 kernel; at M=16 its four
+  // block-diagonal row blocks cost more MFMA time than the LDS-ring tile).
+  if (m <= kMaxDecM) {
+    ks_status_t r;
+    if (run_dec<T>(c, a, b, s, z, bias, m, n, k, gs, st, &r)) return r;
+  }
   const bool dq = m > kDqMinM && (gs % 64 == 0) && (k % 64 == 0) && (n % 64 == 0) &&
                   aligned(a, 16) && aligned(b, 16) && aligned(s, 4) && aligned(z, 4) &&
                   (m + 127) / 128 < 65536;
@@ -586,10 +594,6 @@ ks_status_t run(void* c_, const void* a_, const void* b_, const void* s_, const 
                                                 static_cast<unsigned>(m)),
                        dim3(kThreads), 0, st, c, a, b, s, z, bias, n, k, gs);
     return KS_SUCCESS;
-  }
-  if (m <= kMaxGemvM) {
-    ks_status_t r;
-    if (run_dec<T>(c, a, b, s, z, bias, m, n, k, gs, st, &r)) return r;
   }
   const int tiles = static_cast<int>((n + kTileN - 1) / kTileN);
   const int64_t kp = k / 2;

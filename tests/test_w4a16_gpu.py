@@ -44,7 +44,7 @@ def check(m, k, n, gs, zero_mode="int69", dt="bf16", seed=0, bias=False):
     return out, ref
 
 
-@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 12, 13, 16])
 @pytest.mark.parametrize("k,n,gs", [(256, 128, 128), (512, 384, 64), (1024, 272, 32),
                                     (4096, 4096, 128), (2048, 1040, 256),
                                     # K/2 not a multiple of a workgroup's rows, N not of 256
