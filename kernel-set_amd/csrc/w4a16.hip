@@ -491,21 +491,21 @@ dec_reduce_kernel(uint16_t* __restrict__ c, const float* __restrict__ ws,
   }
 }
 
-template <typename T, int MB, int WAVES, int RPT>
+template <typename T, int MB, int WAVES, int RPT, int ITER>
 void launch_dec(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_t* s,
                 const uint16_t* z, const uint16_t* bias, int m, int n, int k, int gs, int tiles,
                 int splits, float* ws, hipStream_t st) {
-  hipLaunchKernelGGL((w4dec::dec_kernel<T, MB, WAVES, RPT>), dim3(tiles * splits),
+  hipLaunchKernelGGL((w4dec::dec_kernel<T, MB, WAVES, RPT, ITER>), dim3(tiles * splits),
                      dim3(64 * WAVES), 0, st, c, a, b, s, z, bias, m, n, k,
                      gs, splits, ws);
 }
 
-template <typename T, int WAVES, int RPT>
+template <typename T, int MB, int WAVES, int RPT, int ITER>
 ks_status_t dec_rows(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_t* s,
                      const uint16_t* z, const uint16_t* bias, int64_t m, int64_t n, int64_t k,
                      int gs, hipStream_t st) {
   const int tiles = static_cast<int>((n + w4dec::kTileN - 1) / w4dec::kTileN);
-  const int rows_wg = w4dec::Geo<WAVES, RPT>::kRowsWG;
+  const int rows_wg = w4dec::Geo<WAVES, RPT, ITER>::kRowsWG;
   const int splits = static_cast<int>((k / 2 + rows_wg - 1) / rows_wg);
   Scratch sc;
   if (splits > 1) {
@@ -514,14 +514,28 @@ ks_status_t dec_rows(uint16_t* c, const uint16_t* a, const uint8_t* b, const uin
     if (r != KS_SUCCESS) return r;
   }
   const int ni = static_cast<int>(n), ki = static_cast<int>(k), mi = static_cast<int>(m);
-  if (m <= 4)
-    launch_dec<T, 1, WAVES, RPT>(c, a, b, s, z, bias, mi, ni, ki, gs, tiles, splits, sc.partial, st);
-  else
-    launch_dec<T, 2, WAVES, RPT>(c, a, b, s, z, bias, mi, ni, ki, gs, tiles, splits, sc.partial, st);
+  launch_dec<T, MB, WAVES, RPT, ITER>(c, a, b, s, z, bias, mi, ni, ki, gs, tiles, splits,
+                                      sc.partial, st);
   if (splits > 1)
     hipLaunchKernelGGL((dec_reduce_kernel<T>), dim3(tiles), dim3(w4dec::kTileN), 0, st, c,
                        sc.partial, bias, mi, ni, splits, tiles);
   return KS_SUCCESS;
+}
+
+// Row blocks and K chunks per workgroup by shape. Measured on MI355X (K=4096,
+// graph replay, cold): M <= 4 is fastest with one chunk (16 splits); M = 5..8
+// with two chunks once one chunk would give >= 512 workgroups (N=14336 M=8:
+// 14.7 us against 16.2 us), else one (N=4096 M=8: 9.8 us against 10.1 us).
+template <typename T, int WAVES, int RPT>
+ks_status_t dec_dispatch(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_t* s,
+                         const uint16_t* z, const uint16_t* bias, int64_t m, int64_t n,
+                         int64_t k, int gs, hipStream_t st) {
+  if (m <= 4) return dec_rows<T, 1, WAVES, RPT, 1>(c, a, b, s, z, bias, m, n, k, gs, st);
+  const int64_t tiles = (n + w4dec::kTileN - 1) / w4dec::kTileN;
+  const int64_t rows1 = w4dec::Geo<WAVES, RPT, 1>::kRowsWG;
+  const int64_t wgs1 = tiles * ((k / 2 + rows1 - 1) / rows1);
+  if (wgs1 >= 512) return dec_rows<T, 2, WAVES, RPT, 2>(c, a, b, s, z, bias, m, n, k, gs, st);
+  return dec_rows<T, 2, WAVES, RPT, 1>(c, a, b, s, z, bias, m, n, k, gs, st);
 }
 
 // Decode shapes (M <= 8) on MFMA; returns false when the shape or alignment
@@ -538,11 +552,11 @@ bool run_dec(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_t* s
   // workgroups, 16 splits) beats 8 waves x 4 rows, 4 waves x 4 rows and
   // 8 waves x 8 rows (fewer workgroups).
   if (gs % 64 == 0 && k % 64 == 0) {
-    *r = dec_rows<T, 4, 8>(c, a, b, s, z, bias, m, n, k, gs, st);
+    *r = dec_dispatch<T, 4, 8>(c, a, b, s, z, bias, m, n, k, gs, st);
     return true;
   }
   if (gs % 32 == 0 && k % 32 == 0) {
-    *r = dec_rows<T, 4, 4>(c, a, b, s, z, bias, m, n, k, gs, st);
+    *r = dec_dispatch<T, 4, 4>(c, a, b, s, z, bias, m, n, k, gs, st);
     return true;
   }
   return false;
@@ -564,8 +578,9 @@ ks_status_t run(void* c_, const void* a_, const void* b_, const void* s_, const 
                     aligned(a, 16) && aligned(b, 16) && aligned(s, 4) && aligned(z, 4) &&
                     k * n < (int64_t{1} << 40);
   // M <= 8: the MFMA decode kernel (measured on MI355X at K=4096, N=14336:
-  // M=8 15.6 us against 33.3 us for the dot2 kernel; at M=16 its four
-  // block-diagonal row blocks cost more MFMA time than the LDS-ring tile).
+  // M=8 14.7 us against 33.3 us for the dot2 kernel; at M=16, four
+  // block-diagonal row blocks measured 25 us against 18.8 us for the LDS-ring
+  // tile).
   if (m <= kMaxDecM) {
     ks_status_t r;
     if (run_dec<T>(c, a, b, s, z, bias, m, n, k, gs, st, &r)) return r;

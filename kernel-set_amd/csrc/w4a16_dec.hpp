@@ -44,10 +44,11 @@ using w4mma::u32x4v;
 
 constexpr int kTileN = 256;
 
-template <int WAVES, int RPT>
+template <int WAVES, int RPT, int ITER>
 struct Geo {
   static constexpr int kThreads = 64 * WAVES;
-  static constexpr int kRowsWG = WAVES * 4 * RPT;  // packed rows per workgroup
+  static constexpr int kRowsChunk = WAVES * 4 * RPT;      // packed rows per chunk
+  static constexpr int kRowsWG = kRowsChunk * ITER;       // packed rows per workgroup
 };
 
 // Workgroup id -> (column tile, k split); the splits of one tile share an XCD
@@ -74,13 +75,18 @@ __device__ inline uint32_t opaque(uint32_t x) {
 
 // Requirements (checked by the host): n % 16 == 0, k % (8*RPT) == 0,
 // gs % (8*RPT) == 0, A 16-byte aligned with k % 8 == 0, b/s/z 16-byte aligned.
-template <typename T, int MB, int WAVES, int RPT>
+//
+// A workgroup's K range is ITER chunks; in chunk `it` wave w owns packed rows
+// split*kRowsWG + it*kRowsChunk + w*4*RPT .. +4*RPT (8*RPT k, inside one
+// quantization group). Chunk it+1's loads are issued before chunk it's math,
+// and every chunk is promoted with its own group's scales and zeros.
+template <typename T, int MB, int WAVES, int RPT, int ITER>
 __global__ void __launch_bounds__(64 * WAVES)
 dec_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
            const uint8_t* __restrict__ b, const uint16_t* __restrict__ scales,
            const uint16_t* __restrict__ zeros, const uint16_t* __restrict__ bias,
            int m_rows, int n, int k, int gs, int splits, float* __restrict__ ws) {
-  using G = Geo<WAVES, RPT>;
+  using G = Geo<WAVES, RPT, ITER>;
   constexpr int kRowsM = 4 * MB;
   __shared__ float red[WAVES][kRowsM][kTileN];
 
@@ -91,121 +97,145 @@ dec_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
   const int li = lane % 16, g = lane / 16;
   const int col0 = tile * kTileN + 16 * li;
   const int kph = k / 2;
-  const int wrow0 = split * G::kRowsWG + wave * 4 * RPT;  // first packed row of the wave
-  const int row0 = wrow0 + g * RPT;                        // this lane's RPT rows
-  const bool col_ok = col0 < n;
-  const bool rows_ok = row0 < kph;  // k % (8*RPT) == 0: a lane's rows are all in or all out
-
-  // Every load below is unconditional (addresses clamped into the tensors) so
-  // the loads stay branch-free and the math on row i waits only for load i.
-  // Rows past K get zero activations (no contribution); columns past N are
-  // computed on clamped data and never stored.
-  const int crow0 = rows_ok ? row0 : 0;
-  const int ccol0 = col_ok ? col0 : 0;
-
-  // Activation pairs for this lane's MFMA rows: mm = 4*mb + (li / 4). Raw
-  // loads here; rows past M or K are zeroed after every load is issued.
-  const int cdw = li & 3;
-  uint4 araw[MB][RPT / 4];
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    const int mm = 4 * mb + (li >> 2);
-    const uint4* src =
-        reinterpret_cast<const uint4*>(a + static_cast<int64_t>(mm < m_rows ? mm : 0) * k) + crow0 / 4;
-#pragma unroll
-    for (int i = 0; i < RPT / 4; ++i) araw[mb][i] = src[i];
-  }
-  // Scales and zeros of the wave's group, 16 columns per lane (a NULL zeros
-  // pointer reads the scales and is replaced by 0).
   const int ng = k / gs;
-  const int grp = min((2 * wrow0) / gs, ng - 1);
-  const int64_t gi = static_cast<int64_t>(grp) * n + ccol0;
+  const bool col_ok = col0 < n;
+  // Every load is unconditional (addresses clamped into the tensors) so the
+  // loads stay branch-free and the math on row i waits only for load i. Rows
+  // past K get zero activations (no contribution); columns past N are computed
+  // on clamped data and never stored. A NULL zeros pointer reads the scales
+  // and is replaced by 0.
+  const int ccol0 = col_ok ? col0 : 0;
   const uint16_t* zsrc = zeros ? zeros : scales;
-  const uint4 s4[2] = {*reinterpret_cast<const uint4*>(scales + gi),
-                       *reinterpret_cast<const uint4*>(scales + gi + 8)};
-  uint4 z4[2] = {*reinterpret_cast<const uint4*>(zsrc + gi),
-                 *reinterpret_cast<const uint4*>(zsrc + gi + 8)};
-  // The weight stream, nontemporal, all loads in flight before any math.
-  uint4 w[RPT];
+
+  struct Chunk {
+    uint4 a[MB][RPT / 4];  // activation pairs of this lane's RPT rows, raw
+    uint4 s[2], z[2];      // the chunk's group: 16 columns of scales / zeros
+    uint4 w[RPT];          // the weight stream
+    bool rows_ok;
+  };
+  auto issue = [&](int it, Chunk& ch) {
+    const int wrow0 = split * G::kRowsWG + it * G::kRowsChunk + wave * 4 * RPT;
+    const int row0 = wrow0 + g * RPT;
+    ch.rows_ok = row0 < kph;  // k % (8*RPT) == 0: a lane's rows are all in or all out
+    const int crow0 = ch.rows_ok ? row0 : 0;
 #pragma unroll
-  for (int i = 0; i < RPT; ++i)
-    w[i] = load_stream16(b + static_cast<int64_t>(crow0 + i) * n + ccol0);
-  __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the math
-  if (!zeros) z4[0] = z4[1] = make_uint4(0, 0, 0, 0);
-  uint32_t ap[MB][RPT];
+    for (int mb = 0; mb < MB; ++mb) {
+      const int mm = 4 * mb + (li >> 2);
+      const uint4* src = reinterpret_cast<const uint4*>(
+                             a + static_cast<int64_t>(mm < m_rows ? mm : 0) * k) + crow0 / 4;
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    const bool ok = rows_ok && (4 * mb + (li >> 2)) < m_rows;
-#pragma unroll
-    for (int i = 0; i < RPT; i += 4) {
-      const uint4 v = araw[mb][i / 4];
-      ap[mb][i] = ok ? v.x : 0u;
-      ap[mb][i + 1] = ok ? v.y : 0u;
-      ap[mb][i + 2] = ok ? v.z : 0u;
-      ap[mb][i + 3] = ok ? v.w : 0u;
+      for (int i = 0; i < RPT / 4; ++i) ch.a[mb][i] = src[i];
     }
-  }
+    const int grp = min((2 * wrow0) / gs, ng - 1);
+    const int64_t gi = static_cast<int64_t>(grp) * n + ccol0;
+    ch.s[0] = *reinterpret_cast<const uint4*>(scales + gi);
+    ch.s[1] = *reinterpret_cast<const uint4*>(scales + gi + 8);
+    ch.z[0] = *reinterpret_cast<const uint4*>(zsrc + gi);
+    ch.z[1] = *reinterpret_cast<const uint4*>(zsrc + gi + 8);
+#pragma unroll
+    for (int i = 0; i < RPT; ++i)
+      ch.w[i] = load_stream16(b + static_cast<int64_t>(crow0 + i) * n + ccol0);
+  };
 
   // Per-lane perm selectors placing a_even / a_odd into the slots of column cdw.
+  const int cdw = li & 3;
   constexpr uint32_t Z = 0x0c0c0c0cu, EL = 0x0c0c0100u, EH = 0x01000c0cu, OL = 0x0c0c0302u,
                      OH = 0x03020c0cu;
   const uint32_t sel0 = cdw == 0 ? EL : (cdw == 2 ? EH : Z);
   const uint32_t sel1 = cdw == 1 ? EL : (cdw == 3 ? EH : Z);
   const uint32_t sel2 = cdw == 0 ? OL : (cdw == 2 ? OH : Z);
   const uint32_t sel3 = cdw == 1 ? OL : (cdw == 3 ? OH : Z);
-
   const uint32_t base = opaque(w4mma::mfma_traits<T>::magic);
   const uint32_t mask = __builtin_amdgcn_readfirstlane(0x000f000fu);
   const uint32_t one2 = opaque(w4mma::mfma_traits<T>::one2);
   const u32x4v ones = {one2, one2, one2, one2};
-  f32x4 P[MB][4], S[MB];
+  constexpr float u = w4mma::code_scale<T>::unit;
+
+  // Lane holds D[4*(lane/16) + r][li] -> activation row 4*mb + g, column
+  // col0 + 4*p + r; O accumulates the promoted chunks.
+  f32x4 O[MB][4];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    S[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-    for (int p = 0; p < 4; ++p) P[mb][p] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
+    for (int p = 0; p < 4; ++p) O[mb][p] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  Chunk cur;
+  issue(0, cur);
 #pragma unroll
-  for (int i = 0; i < RPT; ++i) {
-    u32x4v af[MB];
+  for (int it = 0; it < ITER; ++it) {
+    Chunk nxt;
+    if (it + 1 < ITER) issue(it + 1, nxt);
+    __builtin_amdgcn_sched_barrier(0);  // next chunk's loads stay ahead of this math
+
+    uint32_t ap[MB][RPT];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
-      const uint32_t x = ap[mb][i];
-      af[mb] = u32x4v{__builtin_amdgcn_perm(x, x, sel0), __builtin_amdgcn_perm(x, x, sel1),
-                      __builtin_amdgcn_perm(x, x, sel2), __builtin_amdgcn_perm(x, x, sel3)};
+      const bool ok = cur.rows_ok && (4 * mb + (li >> 2)) < m_rows;
+#pragma unroll
+      for (int i = 0; i < RPT; i += 4) {
+        const uint4 v = cur.a[mb][i / 4];
+        ap[mb][i] = ok ? v.x : 0u;
+        ap[mb][i + 1] = ok ? v.y : 0u;
+        ap[mb][i + 2] = ok ? v.z : 0u;
+        ap[mb][i + 3] = ok ? v.w : 0u;
+      }
     }
-    const uint32_t dw[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
+    f32x4 P[MB][4], S[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      S[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int p = 0; p < 4; ++p) P[mb][p] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      u32x4v af[MB];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const uint32_t x = ap[mb][i];
+        af[mb] = u32x4v{__builtin_amdgcn_perm(x, x, sel0), __builtin_amdgcn_perm(x, x, sel1),
+                        __builtin_amdgcn_perm(x, x, sel2), __builtin_amdgcn_perm(x, x, sel3)};
+      }
+      const uint32_t dw[4] = {cur.w[i].x, cur.w[i].y, cur.w[i].z, cur.w[i].w};
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const uint32_t d = dw[p];
+        const u32x4v bf = {and_or(d, mask, base), and_or(d >> 8, mask, base),
+                           and_or(d >> 4, mask, base), and_or(d >> 12, mask, base)};
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) P[mb][p] = w4mma::mfma_traits<T>::mma(af[mb], bf, P[mb][p]);
+      }
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) S[mb] = w4mma::mfma_traits<T>::mma(af[mb], ones, S[mb]);
+    }
+    // Promotion with the chunk's group: O += s * (P - (128 + z) * S).
+    const uint32_t sv[8] = {cur.s[0].x, cur.s[0].y, cur.s[0].z, cur.s[0].w,
+                            cur.s[1].x, cur.s[1].y, cur.s[1].z, cur.s[1].w};
+    const uint32_t zv[8] = {cur.z[0].x, cur.z[0].y, cur.z[0].z, cur.z[0].w,
+                            cur.z[1].x, cur.z[1].y, cur.z[1].z, cur.z[1].w};
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
-      const uint32_t d = dw[p];
-      const u32x4v bf = {and_or(d, mask, base), and_or(d >> 8, mask, base),
-                         and_or(d >> 4, mask, base), and_or(d >> 12, mask, base)};
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) P[mb][p] = w4mma::mfma_traits<T>::mma(af[mb], bf, P[mb][p]);
+      for (int r = 0; r < 4; ++r) {
+        const int j = 4 * p + r;
+        const float sj = elem<T>::to_f32(static_cast<uint16_t>(sv[j / 2] >> (16 * (j & 1))));
+        const float zj = zeros ? elem<T>::to_f32(static_cast<uint16_t>(zv[j / 2] >> (16 * (j & 1))))
+                               : 0.f;
+        const float cz = 128.0f + zj * u;
+        const float se = sj * (1.0f / u);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) O[mb][p][r] = fmaf(se, fmaf(-cz, S[mb][r], P[mb][p][r]), O[mb][p][r]);
+      }
     }
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) S[mb] = w4mma::mfma_traits<T>::mma(af[mb], ones, S[mb]);
+    if (it + 1 < ITER) cur = nxt;
   }
 
-  // Promotion: lane holds D[4*(lane/16) + r][li] -> activation row 4*mb + g,
-  // column col0 + 4*p + r.
-  constexpr float u = w4mma::code_scale<T>::unit;
-  const uint32_t sv[8] = {s4[0].x, s4[0].y, s4[0].z, s4[0].w, s4[1].x, s4[1].y, s4[1].z, s4[1].w};
-  const uint32_t zv[8] = {z4[0].x, z4[0].y, z4[0].z, z4[0].w, z4[1].x, z4[1].y, z4[1].z, z4[1].w};
 #pragma unroll
-  for (int p = 0; p < 4; ++p) {
+  for (int p = 0; p < 4; ++p)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int j = 4 * p + r;
-      const float sj = elem<T>::to_f32(static_cast<uint16_t>(sv[j / 2] >> (16 * (j & 1))));
-      const float zj = elem<T>::to_f32(static_cast<uint16_t>(zv[j / 2] >> (16 * (j & 1))));
-      const float cz = 128.0f + zj * u;
-      const float se = sj * (1.0f / u);
+    for (int r = 0; r < 4; ++r)
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb)
-        red[wave][4 * mb + g][16 * li + j] = se * fmaf(-cz, S[mb][r], P[mb][p][r]);
-    }
-  }
+      for (int mb = 0; mb < MB; ++mb) red[wave][4 * mb + g][16 * li + 4 * p + r] = O[mb][p][r];
   __syncthreads();
 
   // Sum the waves in order; one thread per (row, column) entry.
