@@ -406,11 +406,13 @@ ks_status_t run_pipe(uint16_t* c, const uint16_t* a, const uint8_t* b, const uin
   const int tiles = static_cast<int>((n + w4pipe::kTileN - 1) / w4pipe::kTileN);
   const int total = static_cast<int>(k / w4pipe::kStageK);
   const int spg = std::max(1, gs / w4pipe::kStageK);  // splits stay on group boundaries
-  // ~512 workgroups (two per CU), splits aligned to quantization groups and at
-  // least 8 stages long so the ring fill is amortized.
-  int splits = std::max(1, (512 + tiles - 1) / tiles);
+  // ~448 workgroups, splits aligned to quantization groups and at least 4
+  // stages long. Measured on MI355X (K=4096, M=16/64): N=4096 10.1/17.1 us
+  // (13.0/20.0 us with an 8-stage minimum, which left 128 workgroups);
+  // N=14336 18.6/30.7 us (896 workgroups were slower).
+  int splits = std::max(1, (448 + tiles - 1) / tiles);
   int sps = (total + splits - 1) / splits;
-  sps = std::max(sps, std::min(total, 8));
+  sps = std::max(sps, std::min(total, 4));
   sps = ((sps + spg - 1) / spg) * spg;
   splits = (total + sps - 1) / sps;
   const int64_t pass_rows = m > 32 ? 64 : (m > 16 ? 32 : 16);
