@@ -181,8 +181,12 @@ void run(void* c_, const void* a_, const void* b_, const void* s_, const void* z
   const bool pipe = (gs % 64 == 0) && (k % w4pipe::kStageK == 0) && (n % 16 == 0) && aligned(a, 16) &&
                     aligned(b, 16) && aligned(s, 4) && aligned(z, 4);
   if (pipe) {
+    // Pass height from the average rows per expert: an expert taller than a
+    // pass re-reads its weights, a pass taller than the expert multiplies
+    // padding rows (the kernel is MFMA-bound at these shapes).
     if (avg <= 16) launch_pipe<T, 1>(c, a, b, s, z, offs, E, rows, n, k, gs, st);
     else if (avg <= 32) launch_pipe<T, 2>(c, a, b, s, z, offs, E, rows, n, k, gs, st);
+    else if (avg <= 48) launch_pipe<T, 3>(c, a, b, s, z, offs, E, rows, n, k, gs, st);
     else launch_pipe<T, 4>(c, a, b, s, z, offs, E, rows, n, k, gs, st);
     return;
   }

@@ -49,7 +49,7 @@ template <int MB>
 struct Ring {
   static constexpr int kABytes = 16 * MB * 256;
   static constexpr int kSlot = kWBytes + kABytes + kSZBytes;
-  static constexpr int kDepth = MB >= 4 ? 3 : (MB == 2 ? 4 : 6);
+  static constexpr int kDepth = MB >= 3 ? 3 : (MB == 2 ? 4 : 6);  // <= ~75 KB: two workgroups per CU
   static constexpr int kBytes = kSlot * kDepth;
   static constexpr int kALoads = MB;  // 16-byte A loads per thread per stage
   // global_load_lds instructions per thread per stage (identical in every wave)
