@@ -22,25 +22,12 @@
 #include "kernel_set/gemm.h"
 #include "kernel_set/testing.h"
 #include "ks_common.hpp"
+#include "gemm8_common.hpp"
+#include "gemm8_skinny.hpp"
+#include "workspace.hpp"
 
 namespace ks {
 namespace gemm8 {
-
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef int i32x4 __attribute__((ext_vector_type(4)));
-typedef int i32x8 __attribute__((ext_vector_type(8)));
-
-constexpr int kThreads = 256;
-constexpr int kBM = 128, kBN = 128, kBK = 128;
-constexpr int kLdsStride = kBK + 16;  // bytes per LDS row (16 B pad vs bank conflicts)
-
-// FP8_*: blockwise-scaled (ks_gemm_fp8_blockwise); FP8P_*: plain fp32
-// accumulation over all of K with per-token/per-channel scales (ks_gemm_fp8).
-enum Kind { FP8_E4M3 = 0, FP8_E5M2 = 1, INT8 = 2, INT8_RAW = 3, FP8P_E4M3 = 4, FP8P_E5M2 = 5 };
-
-constexpr bool is_fp8_block(int kind) { return kind == FP8_E4M3 || kind == FP8_E5M2; }
-constexpr bool is_fp8_plain(int kind) { return kind == FP8P_E4M3 || kind == FP8P_E5M2; }
-constexpr int fp8_fmt(int kind) { return (kind == FP8_E5M2 || kind == FP8P_E5M2) ? 1 : 0; }
 
 // 4x4 byte transpose: in[r] holds bytes (r,0..3); out[c] holds bytes (0..3,c).
 __device__ inline void transpose4x4(const uint32_t in[4], uint32_t out[4]) {
@@ -60,18 +47,6 @@ __device__ inline void store_out(typename Out::storage* p, float v) {
   *p = elem<Out>::from_f32(v);
 }
 
-struct Args {
-  void* out;
-  const uint8_t* a;
-  const uint8_t* b;
-  const float* a_scale;
-  const float* b_scale;
-  const void* bias;
-  int64_t m, n, k;
-  int block_n, block_k;    // fp8 blockwise
-  int64_t nkb, nnb;        // scale grid dims
-  int a_per_token, b_per_channel;  // w8a8
-};
 
 // Workgroup id -> (tile_m, tile_n). Tiles are walked column-major in groups so
 // that concurrently running workgroups share B column panels in L2.
@@ -715,6 +690,57 @@ inline unsigned simple_grid(const Args& p) {
   return static_cast<unsigned>((p.m * p.n + kThreads - 1) / kThreads);
 }
 
+// Decode shapes (M <= 16) take the skinny kernel: B streamed once, K split
+// over enough workgroups to fill the chip, partials reduced in split order.
+inline bool skinny_ok(const Args& p) {
+  return p.m <= skinny::kMaxM && p.n % 16 == 0 && p.k % skinny::kChunk == 0 &&
+         p.m * p.k < (int64_t{1} << 31) && p.k * p.n < (int64_t{1} << 31) &&
+         (p.k / skinny::kChunk) * p.m * p.n < (int64_t{1} << 31) &&
+         (reinterpret_cast<uintptr_t>(p.a) & 7u) == 0 && (reinterpret_cast<uintptr_t>(p.b) & 15u) == 0;
+}
+
+template <int KIND, typename Out, int MB, int CH>
+ks_status_t launch_skinny(Args p, hipStream_t s, const char* who) {
+  const int64_t tiles = (p.n + skinny::kTileN - 1) / skinny::kTileN;
+  const int64_t kwg = static_cast<int64_t>(skinny::kWaves) * CH * skinny::kChunk;
+  p.splits = static_cast<int>((p.k + kwg - 1) / kwg);
+  Scratch sc;
+  ks_status_t st = get_scratch(s, static_cast<size_t>(p.splits) * p.m * p.n, 0, &sc, who);
+  if (st != KS_SUCCESS) return st;
+  p.ws = sc.partial;
+  hipLaunchKernelGGL((skinny::skinny_kernel<KIND, MB, CH>), dim3(static_cast<unsigned>(tiles * p.splits)),
+                     dim3(skinny::kThreads), 0, s, p);
+  hipLaunchKernelGGL((skinny::skinny_reduce_kernel<KIND, Out>),
+                     dim3(static_cast<unsigned>((p.m * p.n + 255) / 256)), dim3(256), 0, s, p);
+  return KS_SUCCESS;
+}
+
+// Two chunks per wave (512 k-rows per workgroup) once that still gives >= 384
+// workgroups, else one.
+template <int KIND, typename Out, int MB>
+ks_status_t skinny_chunks(const Args& p, hipStream_t s, const char* who) {
+  const int64_t tiles = (p.n + skinny::kTileN - 1) / skinny::kTileN;
+  const int64_t kwg2 = int64_t{2} * skinny::kWaves * skinny::kChunk;
+  if (tiles * ((p.k + kwg2 - 1) / kwg2) >= 384) return launch_skinny<KIND, Out, MB, 2>(p, s, who);
+  return launch_skinny<KIND, Out, MB, 1>(p, s, who);
+}
+
+template <int KIND, typename Out>
+ks_status_t run_skinny(const Args& p, hipStream_t s, const char* who) {
+  if (p.m <= 4) return skinny_chunks<KIND, Out, 1>(p, s, who);
+  if (p.m <= 8) return skinny_chunks<KIND, Out, 2>(p, s, who);
+  return skinny_chunks<KIND, Out, 4>(p, s, who);
+}
+
+template <int KIND>
+ks_status_t run_skinny_out(const Args& p, ks_dtype_t out_dtype, hipStream_t s, const char* who) {
+  switch (out_dtype) {
+    case KS_DTYPE_F32: return run_skinny<KIND, f32_t>(p, s, who);
+    case KS_DTYPE_F16: return run_skinny<KIND, f16_t>(p, s, who);
+    default: return run_skinny<KIND, bf16_t>(p, s, who);
+  }
+}
+
 template <typename Out>
 void run_fp8(const Args& p, ks_dtype_t fp8, hipStream_t s) {
   const bool tiled = tiled_ok(p) && p.block_k % kBK == 0;
@@ -798,6 +824,14 @@ ks_status_t ks_gemm_fp8_blockwise(void* out, const void* a_fp8, const void* b_fp
   p.nkb = (k + block_k - 1) / block_k;
   p.nnb = (n + block_n - 1) / block_n;
   auto s = to_stream(stream);
+  if (skinny_ok(p) && block_k % skinny::kChunk == 0 && block_n % 16 == 0) {
+    const ks_status_t st = fp8_dtype == KS_DTYPE_F8E4M3
+        ? run_skinny_out<FP8_E4M3>(p, out_dtype, s, "ks_gemm_fp8_blockwise")
+        : run_skinny_out<FP8_E5M2>(p, out_dtype, s, "ks_gemm_fp8_blockwise");
+    if (st != KS_SUCCESS) return st;
+    KS_LAUNCH_STATUS("ks_gemm_fp8_blockwise");
+    return KS_SUCCESS;
+  }
   switch (out_dtype) {
     case KS_DTYPE_F32: run_fp8<f32_t>(p, fp8_dtype, s); break;
     case KS_DTYPE_F16: run_fp8<f16_t>(p, fp8_dtype, s); break;
@@ -839,6 +873,14 @@ ks_status_t ks_gemm_fp8(void* out, const void* a_fp8, const void* b_fp8, const f
   p.a_per_token = a_mode == KS_QUANT_PER_TOKEN;
   p.b_per_channel = b_mode == KS_QUANT_PER_CHANNEL;
   auto s = to_stream(stream);
+  if (skinny_ok(p)) {
+    const ks_status_t st = fp8_dtype == KS_DTYPE_F8E4M3
+        ? run_skinny_out<FP8P_E4M3>(p, out_dtype, s, "ks_gemm_fp8")
+        : run_skinny_out<FP8P_E5M2>(p, out_dtype, s, "ks_gemm_fp8");
+    if (st != KS_SUCCESS) return st;
+    KS_LAUNCH_STATUS("ks_gemm_fp8");
+    return KS_SUCCESS;
+  }
   switch (out_dtype) {
     case KS_DTYPE_F32: run_fp8_plain<f32_t>(p, fp8_dtype, s); break;
     case KS_DTYPE_F16: run_fp8_plain<f16_t>(p, fp8_dtype, s); break;
@@ -879,6 +921,12 @@ ks_status_t ks_gemm_w8a8(void* c, const void* a_i8, const void* b_i8, const floa
   p.a_per_token = a_mode == KS_QUANT_PER_TOKEN;
   p.b_per_channel = b_mode == KS_QUANT_PER_CHANNEL;
   auto s = to_stream(stream);
+  if (skinny_ok(p)) {
+    const ks_status_t st = run_skinny_out<INT8>(p, out_dtype, s, "ks_gemm_w8a8");
+    if (st != KS_SUCCESS) return st;
+    KS_LAUNCH_STATUS("ks_gemm_w8a8");
+    return KS_SUCCESS;
+  }
   switch (out_dtype) {
     case KS_DTYPE_F32: run_w8a8<INT8, f32_t>(p, s); break;
     case KS_DTYPE_F16: run_w8a8<INT8, f16_t>(p, s); break;
@@ -901,7 +949,12 @@ ks_status_t ks_testing_gemm_w8a8_i32(int32_t* acc, const void* a_i8, const void*
   p.a = static_cast<const uint8_t*>(a_i8);
   p.b = static_cast<const uint8_t*>(b_i8);
   p.m = m; p.n = n; p.k = k;
-  run_w8a8<INT8_RAW, f32_t>(p, to_stream(stream));
+  if (skinny_ok(p)) {
+    const ks_status_t st = run_skinny<INT8_RAW, f32_t>(p, to_stream(stream), "ks_testing_gemm_w8a8_i32");
+    if (st != KS_SUCCESS) return st;
+  } else {
+    run_w8a8<INT8_RAW, f32_t>(p, to_stream(stream));
+  }
   KS_LAUNCH_STATUS("ks_testing_gemm_w8a8_i32");
   return KS_SUCCESS;
 }

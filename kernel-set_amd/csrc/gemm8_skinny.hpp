@@ -1,0 +1,277 @@
+// kernel-set (MI355X build) -- 8-bit GEMMs for decode shapes (M <= 16):
+// ks_gemm_fp8_blockwise, ks_gemm_fp8 and ks_gemm_w8a8 when A has few rows.
+//
+// At these shapes the call streams B ([K, N], N contiguous) once from HBM and
+// the MFMA work is small, so the kernel feeds B's bytes to the MFMA exactly as
+// they are loaded, with no transpose and no LDS staging:
+//
+//  * Lane (li = lane % 16, g = lane / 16) loads 16 bytes = 16 columns of one
+//    k-row; the 16 lanes of a lane group cover 256 contiguous bytes of that
+//    row, and lane group g takes k-rows 8g..8g+7 of a 32-row chunk.
+//  * Dword p of the 16-byte load holds columns 16*li + 4p + c (c = 0..3) of
+//    its row. The lane's dword p from its 8 rows is an MFMA B operand of 32
+//    byte slots, slot 4r + c = B[row r, column 16*li + 4p + c].
+//  * The A operand is block-diagonal: MFMA row i = 4*q + c (q = activation row
+//    within the fragment, c = column within the dword) carries A[q, row r] in
+//    slot 4r + c and zeros elsewhere. Then D[4q + c][li] is the dot product of
+//    activation row q with column 16*li + 4p + c over the chunk's 32 rows.
+//    Slot order is the same for A and B, so it does not matter how the MFMA
+//    orders its k slots. One v_perm per dword builds the A operand.
+//  * fp8: one v_mfma_scale_f32_16x16x128_f8f6f4 per (row fragment, p);
+//    int8: two v_mfma_i32_16x16x64_i8 (rows 0-3 and 4-7 of the lane group).
+//    One fragment serves 4 activation rows, so M <= 4 costs what M = 1 costs
+//    and M <= 16 uses four fragments.
+//
+// Output lane (li, g) of fragment f holds D rows 4g..4g+3 = activation row
+// 4f + g, columns 16*li + 4p + r. A workgroup's 8 waves take consecutive K
+// ranges of one 256-column tile; they are summed through LDS in a fixed order,
+// and each K split writes a partial plane that skinny_reduce_kernel sums in
+// split order before the epilogue. W8A8 partials are int32 and add exactly,
+// so its results are identical to a single pass.
+//
+// fp8 blockwise (gemm_fp8_blockwise.cu:107-161 of cklxx/kernel-set): each
+// 32-row chunk lies inside one scale block (block_k % 32 == 0); its fp32 chunk
+// partial is promoted as O = fma(P, a_s * b_s, O). The reference promotes per
+// whole block; per-chunk promotion changes only fp32 rounding.
+#pragma once
+
+#include "gemm8_common.hpp"
+
+namespace ks {
+namespace gemm8 {
+namespace skinny {
+
+constexpr int kTileN = 256;   // columns per workgroup
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kChunk = 32;    // k-rows per chunk (8 per lane group)
+constexpr int kMaxM = 16;
+
+// Workgroup id -> (column tile, k split); the splits of one tile share an XCD
+// when the grid divides into the 8 XCDs (ids are dispatched round-robin).
+__device__ inline void map_tile(int bid, int nblocks, int splits, int* tile, int* split) {
+  int logical = bid;
+  if ((nblocks & 7) == 0) logical = (bid & 7) * (nblocks >> 3) + (bid >> 3);
+  *tile = logical / splits;
+  *split = logical % splits;
+}
+
+// Requirements (checked by the host): m <= 4*MB, n % 16 == 0, k % 32 == 0,
+// a 8-byte and b 16-byte aligned, M*K, K*N and splits*M*N below 2^31;
+// blockwise: block_k % 32 == 0, block_n % 16 == 0.
+template <int KIND, int MB, int CH>
+__global__ void __launch_bounds__(kThreads)
+skinny_kernel(Args p) {
+  constexpr bool kInt = KIND == INT8 || KIND == INT8_RAW;
+  constexpr bool kBlock = is_fp8_block(KIND);
+  constexpr int kRows = 4 * MB;
+  __shared__ uint32_t red[kWaves / 2][kRows][kTileN];
+
+  int tile, split;
+  map_tile(blockIdx.x, gridDim.x, p.splits, &tile, &split);
+  const int lane = threadIdx.x % 64;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+  const int li = lane % 16, g = lane / 16;
+  const int m = static_cast<int>(p.m), n = static_cast<int>(p.n), k = static_cast<int>(p.k);
+  const int col = tile * kTileN + 16 * li;
+  const int colc = col < n ? col : n - 16;  // lanes past N load a valid line, store nothing
+  const int kw = (split * kWaves + wave) * CH * kChunk;
+
+  // Activation bytes first (8 per lane per fragment and chunk, L2-resident),
+  // then all of the wave's B bytes (CH * 8 x 16 B per lane): loads complete in
+  // order, so chunk c's math waits only for chunk c's B rows.
+  uint2 av[CH][MB];
+#pragma unroll
+  for (int c = 0; c < CH; ++c)
+#pragma unroll
+    for (int f = 0; f < MB; ++f) {
+      const int am = min(4 * f + li / 4, m - 1);
+      const int ka = min(kw + kChunk * c, k - kChunk) + 8 * g;
+      av[c][f] = *reinterpret_cast<const uint2*>(p.a + static_cast<int64_t>(am) * k + ka);
+    }
+  // Scales of each chunk's block (blockwise): b_scale per lane column group,
+  // a_scale per output row 4f + g of the lane.
+  float bsc[CH], asc[CH][MB];
+  if constexpr (is_fp8_block(KIND)) {
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int kb = min(kw + kChunk * c, k - kChunk) / p.block_k;
+      bsc[c] = p.b_scale[static_cast<int64_t>(kb) * p.nnb + colc / p.block_n];
+#pragma unroll
+      for (int f = 0; f < MB; ++f)
+        asc[c][f] = p.a_scale[static_cast<int64_t>(min(4 * f + g, m - 1)) * p.nkb + kb];
+    }
+  }
+  uint4 bv[CH][8];
+#pragma unroll
+  for (int c = 0; c < CH; ++c)
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const int row = min(kw + kChunk * c + 8 * g + r, k - 1);
+      bv[c][r] = load_stream16(p.b + static_cast<int64_t>(row) * n + colc);
+    }
+  // Keep every load above the math: the scheduler would otherwise sink later
+  // chunks' loads below earlier chunks' MFMAs and serialize their latency.
+  __builtin_amdgcn_sched_barrier(0);
+
+  // A operand selectors: byte r of the lane's 8 activation bytes goes to byte
+  // li % 4 of dword r, the other bytes are zero (v_perm selector 0x0c).
+  const int c4 = li % 4;
+  uint32_t sel[8];
+#pragma unroll
+  for (int r = 0; r < 8; ++r) sel[r] = 0x0c0c0c0cu ^ ((0x0cu ^ r) << (8 * c4));
+
+  typedef typename std::conditional<kInt, i32x4, f32x4>::type acc_t;
+  acc_t acc[MB][4];
+  f32x4 o[MB][4];
+#pragma unroll
+  for (int f = 0; f < MB; ++f)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      acc[f][q] = acc_t{0, 0, 0, 0};
+      o[f][q] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    // A chunk past K (wave-uniform) loaded clamped rows; its A operand is
+    // zeroed so it adds nothing, which keeps every load ahead of the math.
+    const bool chunk_ok = kw + kChunk * c < k;
+    uint32_t fa[MB][8];
+#pragma unroll
+    for (int f = 0; f < MB; ++f) {
+      const bool am_ok = chunk_ok && 4 * f + li / 4 < m;
+      const uint32_t lo = am_ok ? av[c][f].x : 0u, hi = am_ok ? av[c][f].y : 0u;
+#pragma unroll
+      for (int r = 0; r < 8; ++r) fa[f][r] = __builtin_amdgcn_perm(hi, lo, sel[r]);
+    }
+    if constexpr (kBlock) {
+      // fresh chunk partials, promoted with this chunk's scale block
+#pragma unroll
+      for (int f = 0; f < MB; ++f)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[f][q] = acc_t{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      uint32_t bq[8];
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const uint4 v = bv[c][r];
+        bq[r] = q == 0 ? v.x : q == 1 ? v.y : q == 2 ? v.z : v.w;
+      }
+#pragma unroll
+      for (int f = 0; f < MB; ++f) {
+        if constexpr (kInt) {
+          acc[f][q] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+              i32x4{(int)fa[f][0], (int)fa[f][1], (int)fa[f][2], (int)fa[f][3]},
+              i32x4{(int)bq[0], (int)bq[1], (int)bq[2], (int)bq[3]}, acc[f][q], 0, 0, 0);
+          acc[f][q] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+              i32x4{(int)fa[f][4], (int)fa[f][5], (int)fa[f][6], (int)fa[f][7]},
+              i32x4{(int)bq[4], (int)bq[5], (int)bq[6], (int)bq[7]}, acc[f][q], 0, 0, 0);
+        } else {
+          constexpr int fmt = fp8_fmt(KIND);
+          acc[f][q] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+              i32x8{(int)fa[f][0], (int)fa[f][1], (int)fa[f][2], (int)fa[f][3],
+                    (int)fa[f][4], (int)fa[f][5], (int)fa[f][6], (int)fa[f][7]},
+              i32x8{(int)bq[0], (int)bq[1], (int)bq[2], (int)bq[3],
+                    (int)bq[4], (int)bq[5], (int)bq[6], (int)bq[7]},
+              acc[f][q], fmt, fmt, 0, 127, 0, 127);
+        }
+      }
+    }
+    if constexpr (kBlock) {
+#pragma unroll
+      for (int f = 0; f < MB; ++f) {
+        const float sc = asc[c][f] * bsc[c];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o[f][q][r] = fmaf(acc[f][q][r], sc, o[f][q][r]);
+      }
+    }
+  }
+
+  // Sum the 8 waves in a fixed order: (w, w + 4) pairs, then the four pairs.
+  auto val = [&](int f, int q, int r) -> uint32_t {
+    if constexpr (kInt) return static_cast<uint32_t>(acc[f][q][r]);
+    else if constexpr (kBlock) return __float_as_uint(o[f][q][r]);
+    else return __float_as_uint(acc[f][q][r]);
+  };
+  auto add = [](uint32_t x, uint32_t y) -> uint32_t {
+    if constexpr (kInt) return x + y;  // two's-complement int32 add
+    else return __float_as_uint(__uint_as_float(x) + __uint_as_float(y));
+  };
+  if (wave >= kWaves / 2) {
+#pragma unroll
+    for (int f = 0; f < MB; ++f)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[wave - kWaves / 2][4 * f + g][16 * li + 4 * q + r] = val(f, q, r);
+  }
+  __syncthreads();
+  if (wave < kWaves / 2) {
+#pragma unroll
+    for (int f = 0; f < MB; ++f)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          uint32_t& e = red[wave][4 * f + g][16 * li + 4 * q + r];
+          e = add(val(f, q, r), e);
+        }
+  }
+  __syncthreads();
+  uint32_t* ws = static_cast<uint32_t*>(p.ws);
+  for (int e = threadIdx.x; e < kRows * kTileN; e += kThreads) {
+    const int row = e / kTileN, cc = e % kTileN;
+    const int gc = tile * kTileN + cc;
+    if (row >= m || gc >= n) continue;
+    uint32_t v = red[0][row][cc];
+#pragma unroll
+    for (int w = 1; w < kWaves / 2; ++w) v = add(v, red[w][row][cc]);
+    ws[(static_cast<int64_t>(split) * m + row) * n + gc] = v;
+  }
+}
+
+// Sums the split partials in split order, then applies the entry point's
+// epilogue (the same operation order as the tiled kernels).
+template <int KIND, typename Out>
+__global__ void __launch_bounds__(256)
+skinny_reduce_kernel(Args p) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t plane = p.m * p.n;
+  if (idx >= plane) return;
+  const int64_t gm = idx / p.n, gn = idx % p.n;
+  if constexpr (KIND == INT8 || KIND == INT8_RAW) {
+    const int32_t* ws = static_cast<const int32_t*>(p.ws);
+    uint32_t s = 0;
+    for (int sp = 0; sp < p.splits; ++sp) s += static_cast<uint32_t>(ws[sp * plane + idx]);
+    const int32_t acc = static_cast<int32_t>(s);
+    if constexpr (KIND == INT8_RAW) {
+      static_cast<int32_t*>(p.out)[idx] = acc;
+    } else {
+      const float as = p.a_per_token ? p.a_scale[gm] : p.a_scale[0];
+      const float bsc = p.b_per_channel ? p.b_scale[gn] : p.b_scale[0];
+      float v = __fmul_rn(__fmul_rn(static_cast<float>(acc), as), bsc);
+      if (p.bias)
+        v = __fadd_rn(v, elem<Out>::load(static_cast<const typename Out::storage*>(p.bias), gn));
+      static_cast<typename Out::storage*>(p.out)[idx] = elem<Out>::from_f32(v);
+    }
+  } else {
+    const float* ws = static_cast<const float*>(p.ws);
+    float s = 0.f;
+    for (int sp = 0; sp < p.splits; ++sp) s += ws[sp * plane + idx];
+    if constexpr (is_fp8_plain(KIND)) {
+      const float as = p.a_per_token ? p.a_scale[gm] : p.a_scale[0];
+      const float bsc = p.b_per_channel ? p.b_scale[gn] : p.b_scale[0];
+      s = __fmul_rn(__fmul_rn(s, as), bsc);
+    }
+    static_cast<typename Out::storage*>(p.out)[idx] = elem<Out>::from_f32(s);
+  }
+}
+
+}  // namespace skinny
+}  // namespace gemm8
+}  // namespace ks
