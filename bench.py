@@ -8,7 +8,7 @@ one ks_gemm_w4a16 call.
 
 Secondary lines (key ``secondary``) cover every BASELINE config: the fp8
 blockwise GEMM and its 1x128 activation quantizer (config 3, the second half of
-the metric), the W4A16 sweep (config 2), W8A8 (config 4) and the MoE grouped
+the metric; plus the same GEMM at decode M = 1 and M = 64 with cold weights), the W4A16 sweep (config 2), W8A8 (config 4) and the MoE grouped
 W4A16 GEMM (config 5).
 
 Timing: calls are captured into a HIP graph (so host launch overhead is not
@@ -215,6 +215,30 @@ def wl_fp8_plain(torch, ks, H):
     return fn, 8, nbytes, 2.0 * m * n * k
 
 
+def wl_fp8_skinny(torch, ks, H, m, rotate=6):
+    """fp8 blockwise GEMM at decode / small-batch M (N = K = 7168, the config 3
+    width): `rotate` distinct 51 MB weight sets (over the 256 MB MALL at 6) so
+    every call streams B from HBM."""
+    import oracle as O
+    n = k = 7168
+    rng = np.random.default_rng(m)
+    a8 = torch.from_numpy(O.fp8_encode(rng.standard_normal((m, k)).astype(np.float32))).cuda()
+    a_s = torch.from_numpy(rng.uniform(0.001, 0.01, (m, k // 128)).astype(np.float32)).cuda()
+    g = torch.Generator(device="cuda").manual_seed(m)
+    bs = [torch.randint(0, 256, (k, n), device="cuda", dtype=torch.uint8, generator=g)
+          .bitwise_and_(0x77).view(torch.float8_e4m3fn) for _ in range(rotate)]  # finite codes
+    bsc = [torch.rand(k // 128, n // 128, device="cuda", generator=g) * 0.01 + 0.001
+           for _ in range(rotate)]
+    a8 = a8.view(torch.float8_e4m3fn)
+    out = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+
+    def fn(i):
+        ks.gemm.gemm_fp8_blockwise(out, a8, bs[i], a_s, bsc[i], m, n, k)
+
+    nbytes = m * k + k * n + m * n * 2 + a_s.numel() * 4 + bsc[0].numel() * 4
+    return fn, rotate, nbytes, 2.0 * m * n * k
+
+
 def wl_w8a8(torch, ks, H):
     m = n = k = 4096
     rng = np.random.default_rng(8)
@@ -383,6 +407,11 @@ def main():
             fn, per, nb, fl = wl_fp8_plain(torch, ks, H)
             ms2, c2 = T.run(fn, per, max(32, steps // 8), 8, min_per_graph=8)
             sec["fp8_per_token_gemm_M2048_N7168_K7168"] = line("fp8 gemm per-token", ms2, c2, nb, fl, "mfma", "fp8")
+            for mm in (1, 64):  # decode / small batch: HBM-bound (B = 51 MB)
+                fn, per, nb, fl = wl_fp8_skinny(torch, ks, H, mm)
+                ms2, c2 = T.run(fn, per, max(64, steps // 4), 12, min_per_graph=24)
+                sec[f"fp8_blockwise_gemm_M{mm}_N7168_K7168_cold"] = line(
+                    f"fp8 gemm M={mm}", ms2, c2, nb, fl, "hbm")
         if "quant" in only:
             fn, per, nb, fl = wl_quant_group(torch, ks, H, 16)
             ms2, c2 = T.run(fn, per, steps, 32)

@@ -318,7 +318,12 @@ __device__ inline int a_swz(int row) { return (row >> 1) & 7; }
 __device__ inline int b_swz(int row) { return (row & 7) | ((((row >> 4) ^ (row >> 5)) & 1) << 3); }
 typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
 
-template <int KIND, typename Out, bool UNIFORM_BS>
+// SPLIT: workgroup id = tile * p.splits + split; the split runs K steps
+// [split * per, min(steps, (split + 1) * per)) and writes its raw accumulators
+// (fp8 blockwise: the promoted O; plain fp8: the fp32 sum; int8: int32) to the
+// partial plane p.ws, which skinny::skinny_reduce_kernel sums in split order
+// before the epilogue.
+template <int KIND, typename Out, bool UNIFORM_BS, bool SPLIT>
 __global__ void __launch_bounds__(kFThreads)
 gemm8_fast_kernel(Args p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -330,7 +335,12 @@ gemm8_fast_kernel(Args p) {
   const int tiles_m = static_cast<int>((p.m + kFBM - 1) / kFBM);
   const int tiles_n = static_cast<int>(p.n / kFBN);
   int tm, tn;
-  tile_coords(blockIdx.x, tiles_m, tiles_n, &tm, &tn);
+  int bid = blockIdx.x, split = 0;
+  if constexpr (SPLIT) {
+    split = bid % p.splits;
+    bid /= p.splits;
+  }
+  tile_coords(bid, tiles_m, tiles_n, &tm, &tn);
   const int64_t m0 = static_cast<int64_t>(tm) * kFBM;
   const int64_t n0 = static_cast<int64_t>(tn) * kFBN;
 
@@ -402,12 +412,17 @@ gemm8_fast_kernel(Args p) {
     for (int r = 0; r < 4; ++r) o[r] = fmaf(part[r], sc[r], o[r]);
   };
 
-  const int steps = static_cast<int>(p.k / kBK);
-  issue_loads(0, 0);
+  int s_begin = 0, steps = static_cast<int>(p.k / kBK);
+  if constexpr (SPLIT) {
+    const int per = (steps + p.splits - 1) / p.splits;
+    s_begin = split * per;
+    steps = min(steps, s_begin + per);
+  }
+  issue_loads(s_begin, 0);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  for (int s = 0; s < steps; ++s) {
-    const int cur = s & 1;
+  for (int s = s_begin; s < steps; ++s) {
+    const int cur = (s - s_begin) & 1;
     if (s + 1 < steps) issue_loads(s + 1, cur ^ 1);
     const uint8_t* a_src = sA + cur * kFBM * kFARow;
     const uint8_t* b_src = sB + cur * kBK * kFBRow;
@@ -454,7 +469,7 @@ gemm8_fast_kernel(Args p) {
         fb[j] = i32x8{q0[0], q0[1], q1[0], q1[1], q2[0], q2[1], q3[0], q3[1]};
         bs[j] = sBs[cur * kFBN + wn + 16 * j + li];
       }
-      if (s > 0) {
+      if (s > s_begin) {
         promote16(acc_o[7][2], plast[0], UNIFORM_BS ? sclast : sclast * bslast[2]);
         promote16(acc_o[7][3], plast[1], UNIFORM_BS ? sclast : sclast * bslast[3]);
       }
@@ -552,6 +567,25 @@ gemm8_fast_kernel(Args p) {
   }
 
   // ---- epilogue: lane holds rows wm+16i+4lk+r, column wn+16j+li ----
+  if constexpr (SPLIT) {
+    uint32_t* ws = static_cast<uint32_t*>(p.ws) + split * p.m * p.n;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t gn = n0 + wn + 16 * j + li;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t gm = m0 + wm + 16 * i + 4 * lk + r;
+          if (gm >= p.m) continue;
+          if constexpr (KIND == INT8 || KIND == INT8_RAW)
+            ws[gm * p.n + gn] = static_cast<uint32_t>(acc_i[i][j][r]);
+          else
+            ws[gm * p.n + gn] = __float_as_uint(acc_o[i][j][r]);
+        }
+    }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int64_t gn = n0 + wn + 16 * j + li;
@@ -663,35 +697,66 @@ inline bool fast_ok(const Args& p) {
          (reinterpret_cast<uintptr_t>(p.b) & 15u) == 0;
 }
 
-template <int KIND, typename Out, bool UBS>
-void launch_fast_impl(const Args& p, hipStream_t s) {
+template <int KIND, typename Out, bool UBS, bool SPLIT>
+void launch_fast_kernel(const Args& p, int64_t wgs, hipStream_t s) {
   static bool configured = false;  // opt in to the LDS size once per process
   if (!configured) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm8_fast_kernel<KIND, Out, UBS>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm8_fast_kernel<KIND, Out, UBS, SPLIT>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kFastLds));
     configured = true;
   }
-  const int64_t tiles = ((p.m + kFBM - 1) / kFBM) * ((p.n + kFBN - 1) / kFBN);
-  hipLaunchKernelGGL((gemm8_fast_kernel<KIND, Out, UBS>), dim3(static_cast<unsigned>(tiles)),
+  hipLaunchKernelGGL((gemm8_fast_kernel<KIND, Out, UBS, SPLIT>), dim3(static_cast<unsigned>(wgs)),
                      dim3(kFThreads), kFastLds, s, p);
+}
+
+// Fewer tiles than CUs (M <= 512 at N = 7168): split K so tiles * splits
+// fills the 256 CUs (one 130 KB-LDS workgroup each), at least two K steps
+// per split; the splits' raw accumulators are summed in split order by
+// skinny_reduce_kernel, which also applies the epilogue.
+inline int fast_splits(const Args& p) {
+  const int64_t tiles = ((p.m + kFBM - 1) / kFBM) * ((p.n + kFBN - 1) / kFBN);
+  const int64_t steps = p.k / kBK;
+  int64_t sp = std::min<int64_t>(256 / std::max<int64_t>(tiles, 1), steps / 2);
+  if (sp <= 1 || (sp * p.m * p.n) >= (int64_t{1} << 31)) return 1;
+  const int64_t per = (steps + sp - 1) / sp;
+  return static_cast<int>((steps + per - 1) / per);  // every split gets >= 1 step
+}
+
+template <int KIND, typename Out, bool UBS>
+ks_status_t launch_fast_impl(Args p, hipStream_t s) {
+  const int64_t tiles = ((p.m + kFBM - 1) / kFBM) * ((p.n + kFBN - 1) / kFBN);
+  p.splits = fast_splits(p);
+  if (p.splits == 1) {
+    launch_fast_kernel<KIND, Out, UBS, false>(p, tiles, s);
+    return KS_SUCCESS;
+  }
+  Scratch sc;
+  ks_status_t st = get_scratch(s, static_cast<size_t>(p.splits) * p.m * p.n, 0, &sc, "gemm8 split-K");
+  if (st != KS_SUCCESS) return st;
+  p.ws = sc.partial;
+  launch_fast_kernel<KIND, Out, UBS, true>(p, tiles * p.splits, s);
+  hipLaunchKernelGGL((skinny::skinny_reduce_kernel<KIND, Out>),
+                     dim3(static_cast<unsigned>((p.m * p.n + 255) / 256)), dim3(256), 0, s, p);
+  return KS_SUCCESS;
 }
 
 // A wave's 64 columns share one b_scale entry when block_n is a multiple of 64
 // (n0 and the wave offsets are multiples of 64).
 template <int KIND, typename Out>
-void launch_fast(const Args& p, hipStream_t s) {
+ks_status_t launch_fast(const Args& p, hipStream_t s) {
   if ((KIND == FP8_E4M3 || KIND == FP8_E5M2) && p.block_n % 64 == 0)
-    launch_fast_impl<KIND, Out, true>(p, s);
-  else
-    launch_fast_impl<KIND, Out, false>(p, s);
+    return launch_fast_impl<KIND, Out, true>(p, s);
+  return launch_fast_impl<KIND, Out, false>(p, s);
 }
 
 inline unsigned simple_grid(const Args& p) {
   return static_cast<unsigned>((p.m * p.n + kThreads - 1) / kThreads);
 }
 
-// Decode shapes (M <= 16) take the skinny kernel: B streamed once, K split
+// Decode shapes (M <= 8) take the skinny kernel: B streamed once, K split
 // over enough workgroups to fill the chip, partials reduced in split order.
+// From M = 9 the split-K 256x256 kernel is faster (N = K = 7168: M = 16
+// 23.5 us skinny against 22.4 us split-K at M = 17).
 inline bool skinny_ok(const Args& p) {
   return p.m <= skinny::kMaxM && p.n % 16 == 0 && p.k % skinny::kChunk == 0 &&
          p.m * p.k < (int64_t{1} << 31) && p.k * p.n < (int64_t{1} << 31) &&
@@ -715,21 +780,26 @@ ks_status_t launch_skinny(Args p, hipStream_t s, const char* who) {
   return KS_SUCCESS;
 }
 
-// Two chunks per wave (512 k-rows per workgroup) once that still gives >= 384
-// workgroups, else one.
+// Chunks per wave: the most (4, 2, 1) that still gives >= 192 workgroups.
+// Measured on MI355X (graph replay, N = K = 7168, fp8 blockwise): M = 1/4/8
+// 13.7/13.6/15.1 us with 4 chunks against 13.9/14.2/18.0 with 2; at
+// N = K = 4096 only one chunk per wave fills the chip.
 template <int KIND, typename Out, int MB>
 ks_status_t skinny_chunks(const Args& p, hipStream_t s, const char* who) {
   const int64_t tiles = (p.n + skinny::kTileN - 1) / skinny::kTileN;
-  const int64_t kwg2 = int64_t{2} * skinny::kWaves * skinny::kChunk;
-  if (tiles * ((p.k + kwg2 - 1) / kwg2) >= 384) return launch_skinny<KIND, Out, MB, 2>(p, s, who);
+  auto wgs = [&](int ch) {
+    const int64_t kwg = int64_t{ch} * skinny::kWaves * skinny::kChunk;
+    return tiles * ((p.k + kwg - 1) / kwg);
+  };
+  if (wgs(4) >= 192) return launch_skinny<KIND, Out, MB, 4>(p, s, who);
+  if (wgs(2) >= 192) return launch_skinny<KIND, Out, MB, 2>(p, s, who);
   return launch_skinny<KIND, Out, MB, 1>(p, s, who);
 }
 
 template <int KIND, typename Out>
 ks_status_t run_skinny(const Args& p, hipStream_t s, const char* who) {
   if (p.m <= 4) return skinny_chunks<KIND, Out, 1>(p, s, who);
-  if (p.m <= 8) return skinny_chunks<KIND, Out, 2>(p, s, who);
-  return skinny_chunks<KIND, Out, 4>(p, s, who);
+  return skinny_chunks<KIND, Out, 2>(p, s, who);
 }
 
 template <int KIND>
@@ -742,40 +812,43 @@ ks_status_t run_skinny_out(const Args& p, ks_dtype_t out_dtype, hipStream_t s, c
 }
 
 template <typename Out>
-void run_fp8(const Args& p, ks_dtype_t fp8, hipStream_t s) {
+ks_status_t run_fp8(const Args& p, ks_dtype_t fp8, hipStream_t s) {
   const bool tiled = tiled_ok(p) && p.block_k % kBK == 0;
   const bool fast = tiled && p.block_k == kBK && fast_ok(p);
   if (fp8 == KS_DTYPE_F8E4M3) {
-    if (fast) launch_fast<FP8_E4M3, Out>(p, s);
+    if (fast) return launch_fast<FP8_E4M3, Out>(p, s);
     else if (tiled) launch_tiled<FP8_E4M3, Out>(p, s);
     else hipLaunchKernelGGL((fp8_blockwise_simple_kernel<e4m3_t, Out>), dim3(simple_grid(p)), dim3(kThreads), 0, s, p);
   } else {
-    if (fast) launch_fast<FP8_E5M2, Out>(p, s);
+    if (fast) return launch_fast<FP8_E5M2, Out>(p, s);
     else if (tiled) launch_tiled<FP8_E5M2, Out>(p, s);
     else hipLaunchKernelGGL((fp8_blockwise_simple_kernel<e5m2_t, Out>), dim3(simple_grid(p)), dim3(kThreads), 0, s, p);
   }
+  return KS_SUCCESS;
 }
 
 template <typename Out>
-void run_fp8_plain(const Args& p, ks_dtype_t fp8, hipStream_t s) {
+ks_status_t run_fp8_plain(const Args& p, ks_dtype_t fp8, hipStream_t s) {
   const bool tiled = tiled_ok(p);
   const bool fast = tiled && fast_ok(p);
   if (fp8 == KS_DTYPE_F8E4M3) {
-    if (fast) launch_fast<FP8P_E4M3, Out>(p, s);
+    if (fast) return launch_fast<FP8P_E4M3, Out>(p, s);
     else if (tiled) launch_tiled<FP8P_E4M3, Out>(p, s);
     else hipLaunchKernelGGL((fp8_plain_simple_kernel<e4m3_t, Out>), dim3(simple_grid(p)), dim3(kThreads), 0, s, p);
   } else {
-    if (fast) launch_fast<FP8P_E5M2, Out>(p, s);
+    if (fast) return launch_fast<FP8P_E5M2, Out>(p, s);
     else if (tiled) launch_tiled<FP8P_E5M2, Out>(p, s);
     else hipLaunchKernelGGL((fp8_plain_simple_kernel<e5m2_t, Out>), dim3(simple_grid(p)), dim3(kThreads), 0, s, p);
   }
+  return KS_SUCCESS;
 }
 
 template <int KIND, typename Out>
-void run_w8a8(const Args& p, hipStream_t s) {
-  if (tiled_ok(p) && fast_ok(p)) launch_fast<KIND, Out>(p, s);
-  else if (tiled_ok(p)) launch_tiled<KIND, Out>(p, s);
+ks_status_t run_w8a8(const Args& p, hipStream_t s) {
+  if (tiled_ok(p) && fast_ok(p)) return launch_fast<KIND, Out>(p, s);
+  if (tiled_ok(p)) launch_tiled<KIND, Out>(p, s);
   else hipLaunchKernelGGL((w8a8_simple_kernel<KIND, Out>), dim3(simple_grid(p)), dim3(kThreads), 0, s, p);
+  return KS_SUCCESS;
 }
 
 }  // namespace gemm8
@@ -832,11 +905,13 @@ ks_status_t ks_gemm_fp8_blockwise(void* out, const void* a_fp8, const void* b_fp
     KS_LAUNCH_STATUS("ks_gemm_fp8_blockwise");
     return KS_SUCCESS;
   }
+  ks_status_t st = KS_SUCCESS;
   switch (out_dtype) {
-    case KS_DTYPE_F32: run_fp8<f32_t>(p, fp8_dtype, s); break;
-    case KS_DTYPE_F16: run_fp8<f16_t>(p, fp8_dtype, s); break;
-    default: run_fp8<bf16_t>(p, fp8_dtype, s); break;
+    case KS_DTYPE_F32: st = run_fp8<f32_t>(p, fp8_dtype, s); break;
+    case KS_DTYPE_F16: st = run_fp8<f16_t>(p, fp8_dtype, s); break;
+    default: st = run_fp8<bf16_t>(p, fp8_dtype, s); break;
   }
+  if (st != KS_SUCCESS) return st;
   KS_LAUNCH_STATUS("ks_gemm_fp8_blockwise");
   return KS_SUCCESS;
 }
@@ -881,11 +956,13 @@ ks_status_t ks_gemm_fp8(void* out, const void* a_fp8, const void* b_fp8, const f
     KS_LAUNCH_STATUS("ks_gemm_fp8");
     return KS_SUCCESS;
   }
+  ks_status_t st = KS_SUCCESS;
   switch (out_dtype) {
-    case KS_DTYPE_F32: run_fp8_plain<f32_t>(p, fp8_dtype, s); break;
-    case KS_DTYPE_F16: run_fp8_plain<f16_t>(p, fp8_dtype, s); break;
-    default: run_fp8_plain<bf16_t>(p, fp8_dtype, s); break;
+    case KS_DTYPE_F32: st = run_fp8_plain<f32_t>(p, fp8_dtype, s); break;
+    case KS_DTYPE_F16: st = run_fp8_plain<f16_t>(p, fp8_dtype, s); break;
+    default: st = run_fp8_plain<bf16_t>(p, fp8_dtype, s); break;
   }
+  if (st != KS_SUCCESS) return st;
   KS_LAUNCH_STATUS("ks_gemm_fp8");
   return KS_SUCCESS;
 }
@@ -927,11 +1004,13 @@ ks_status_t ks_gemm_w8a8(void* c, const void* a_i8, const void* b_i8, const floa
     KS_LAUNCH_STATUS("ks_gemm_w8a8");
     return KS_SUCCESS;
   }
+  ks_status_t st = KS_SUCCESS;
   switch (out_dtype) {
-    case KS_DTYPE_F32: run_w8a8<INT8, f32_t>(p, s); break;
-    case KS_DTYPE_F16: run_w8a8<INT8, f16_t>(p, s); break;
-    default: run_w8a8<INT8, bf16_t>(p, s); break;
+    case KS_DTYPE_F32: st = run_w8a8<INT8, f32_t>(p, s); break;
+    case KS_DTYPE_F16: st = run_w8a8<INT8, f16_t>(p, s); break;
+    default: st = run_w8a8<INT8, bf16_t>(p, s); break;
   }
+  if (st != KS_SUCCESS) return st;
   KS_LAUNCH_STATUS("ks_gemm_w8a8");
   return KS_SUCCESS;
 }
@@ -953,7 +1032,8 @@ ks_status_t ks_testing_gemm_w8a8_i32(int32_t* acc, const void* a_i8, const void*
     const ks_status_t st = run_skinny<INT8_RAW, f32_t>(p, to_stream(stream), "ks_testing_gemm_w8a8_i32");
     if (st != KS_SUCCESS) return st;
   } else {
-    run_w8a8<INT8_RAW, f32_t>(p, to_stream(stream));
+    const ks_status_t st = run_w8a8<INT8_RAW, f32_t>(p, to_stream(stream));
+    if (st != KS_SUCCESS) return st;
   }
   KS_LAUNCH_STATUS("ks_testing_gemm_w8a8_i32");
   return KS_SUCCESS;

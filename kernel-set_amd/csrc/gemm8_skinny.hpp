@@ -1,4 +1,4 @@
-// kernel-set (MI355X build) -- 8-bit GEMMs for decode shapes (M <= 16):
+// kernel-set (MI355X build) -- 8-bit GEMMs for decode shapes (M <= 8):
 // ks_gemm_fp8_blockwise, ks_gemm_fp8 and ks_gemm_w8a8 when A has few rows.
 //
 // At these shapes the call streams B ([K, N], N contiguous) once from HBM and
@@ -20,7 +20,7 @@
 //  * fp8: one v_mfma_scale_f32_16x16x128_f8f6f4 per (row fragment, p);
 //    int8: two v_mfma_i32_16x16x64_i8 (rows 0-3 and 4-7 of the lane group).
 //    One fragment serves 4 activation rows, so M <= 4 costs what M = 1 costs
-//    and M <= 16 uses four fragments.
+//    and M <= 8 uses two fragments.
 //
 // Output lane (li, g) of fragment f holds D rows 4g..4g+3 = activation row
 // 4f + g, columns 16*li + 4p + r. A workgroup's 8 waves take consecutive K
@@ -45,7 +45,7 @@ constexpr int kTileN = 256;   // columns per workgroup
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kChunk = 32;    // k-rows per chunk (8 per lane group)
-constexpr int kMaxM = 16;
+constexpr int kMaxM = 8;
 
 // Workgroup id -> (column tile, k split); the splits of one tile share an XCD
 // when the grid divides into the 8 XCDs (ids are dispatched round-robin).
@@ -137,57 +137,51 @@ skinny_kernel(Args p) {
     // A chunk past K (wave-uniform) loaded clamped rows; its A operand is
     // zeroed so it adds nothing, which keeps every load ahead of the math.
     const bool chunk_ok = kw + kChunk * c < k;
-    uint32_t fa[MB][8];
+    // One fragment at a time: its A operand (8 perms) and, for blockwise, its
+    // chunk partials live only while its MFMAs run.
 #pragma unroll
     for (int f = 0; f < MB; ++f) {
       const bool am_ok = chunk_ok && 4 * f + li / 4 < m;
       const uint32_t lo = am_ok ? av[c][f].x : 0u, hi = am_ok ? av[c][f].y : 0u;
+      uint32_t fa[8];
 #pragma unroll
-      for (int r = 0; r < 8; ++r) fa[f][r] = __builtin_amdgcn_perm(hi, lo, sel[r]);
-    }
-    if constexpr (kBlock) {
-      // fresh chunk partials, promoted with this chunk's scale block
+      for (int r = 0; r < 8; ++r) fa[r] = __builtin_amdgcn_perm(hi, lo, sel[r]);
+      acc_t part[4];
 #pragma unroll
-      for (int f = 0; f < MB; ++f)
+      for (int q = 0; q < 4; ++q) {
+        uint32_t bq[8];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) acc[f][q] = acc_t{0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      uint32_t bq[8];
-#pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        const uint4 v = bv[c][r];
-        bq[r] = q == 0 ? v.x : q == 1 ? v.y : q == 2 ? v.z : v.w;
-      }
-#pragma unroll
-      for (int f = 0; f < MB; ++f) {
+        for (int r = 0; r < 8; ++r) {
+          const uint4 v = bv[c][r];
+          bq[r] = q == 0 ? v.x : q == 1 ? v.y : q == 2 ? v.z : v.w;
+        }
+        const acc_t cin = kBlock ? acc_t{0, 0, 0, 0} : acc[f][q];
         if constexpr (kInt) {
-          acc[f][q] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-              i32x4{(int)fa[f][0], (int)fa[f][1], (int)fa[f][2], (int)fa[f][3]},
-              i32x4{(int)bq[0], (int)bq[1], (int)bq[2], (int)bq[3]}, acc[f][q], 0, 0, 0);
-          acc[f][q] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-              i32x4{(int)fa[f][4], (int)fa[f][5], (int)fa[f][6], (int)fa[f][7]},
-              i32x4{(int)bq[4], (int)bq[5], (int)bq[6], (int)bq[7]}, acc[f][q], 0, 0, 0);
+          part[q] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+              i32x4{(int)fa[0], (int)fa[1], (int)fa[2], (int)fa[3]},
+              i32x4{(int)bq[0], (int)bq[1], (int)bq[2], (int)bq[3]}, cin, 0, 0, 0);
+          part[q] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+              i32x4{(int)fa[4], (int)fa[5], (int)fa[6], (int)fa[7]},
+              i32x4{(int)bq[4], (int)bq[5], (int)bq[6], (int)bq[7]}, part[q], 0, 0, 0);
         } else {
           constexpr int fmt = fp8_fmt(KIND);
-          acc[f][q] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-              i32x8{(int)fa[f][0], (int)fa[f][1], (int)fa[f][2], (int)fa[f][3],
-                    (int)fa[f][4], (int)fa[f][5], (int)fa[f][6], (int)fa[f][7]},
+          part[q] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+              i32x8{(int)fa[0], (int)fa[1], (int)fa[2], (int)fa[3],
+                    (int)fa[4], (int)fa[5], (int)fa[6], (int)fa[7]},
               i32x8{(int)bq[0], (int)bq[1], (int)bq[2], (int)bq[3],
                     (int)bq[4], (int)bq[5], (int)bq[6], (int)bq[7]},
-              acc[f][q], fmt, fmt, 0, 127, 0, 127);
+              cin, fmt, fmt, 0, 127, 0, 127);
         }
       }
-    }
-    if constexpr (kBlock) {
-#pragma unroll
-      for (int f = 0; f < MB; ++f) {
+      if constexpr (kBlock) {
         const float sc = asc[c][f] * bsc[c];
 #pragma unroll
         for (int q = 0; q < 4; ++q)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) o[f][q][r] = fmaf(acc[f][q][r], sc, o[f][q][r]);
+          for (int r = 0; r < 4; ++r) o[f][q][r] = fmaf(part[q][r], sc, o[f][q][r]);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[f][q] = part[q];
       }
     }
   }
@@ -245,9 +239,16 @@ skinny_reduce_kernel(Args p) {
   if (idx >= plane) return;
   const int64_t gm = idx / p.n, gn = idx % p.n;
   if constexpr (KIND == INT8 || KIND == INT8_RAW) {
-    const int32_t* ws = static_cast<const int32_t*>(p.ws);
+    const uint32_t* ws = static_cast<const uint32_t*>(p.ws) + idx;
     uint32_t s = 0;
-    for (int sp = 0; sp < p.splits; ++sp) s += static_cast<uint32_t>(ws[sp * plane + idx]);
+    for (int sp = 0; sp < p.splits; sp += 8) {  // 8 loads in flight, added in order
+      uint32_t part[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) part[i] = ws[min(sp + i, p.splits - 1) * plane];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (sp + i < p.splits) s += part[i];
+    }
     const int32_t acc = static_cast<int32_t>(s);
     if constexpr (KIND == INT8_RAW) {
       static_cast<int32_t*>(p.out)[idx] = acc;
@@ -260,9 +261,16 @@ skinny_reduce_kernel(Args p) {
       static_cast<typename Out::storage*>(p.out)[idx] = elem<Out>::from_f32(v);
     }
   } else {
-    const float* ws = static_cast<const float*>(p.ws);
+    const float* ws = static_cast<const float*>(p.ws) + idx;
     float s = 0.f;
-    for (int sp = 0; sp < p.splits; ++sp) s += ws[sp * plane + idx];
+    for (int sp = 0; sp < p.splits; sp += 8) {  // 8 loads in flight, added in order
+      float part[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) part[i] = ws[min(sp + i, p.splits - 1) * plane];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (sp + i < p.splits) s += part[i];
+    }
     if constexpr (is_fp8_plain(KIND)) {
       const float as = p.a_per_token ? p.a_scale[gm] : p.a_scale[0];
       const float bsc = p.b_per_channel ? p.b_scale[gn] : p.b_scale[0];

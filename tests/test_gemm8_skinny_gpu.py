@@ -1,13 +1,15 @@
-"""GPU parity of the decode-shape (M <= 16) path of the three 8-bit GEMMs
+"""GPU parity of the decode-shape (M <= 8) path of the three 8-bit GEMMs
 (ks_gemm_fp8_blockwise, ks_gemm_fp8, ks_gemm_w8a8): B streamed once, K split
-over workgroups, split partials summed in order by a second kernel.
+over workgroups, split partials summed in order by a second kernel. M = 9..16
+in the same parametrizations runs the split-K 256x256 kernel (or the tiled
+kernel where N is not a multiple of 256) on the same data, to the same bars.
 
 Same bars as the tiled kernels:
   * fp8 blockwise / plain fp8: max |out - ref| / max |ref| <= 1e-2 against the
     closed-form oracle; exact for integer-valued operands with unit scales;
   * W8A8: int32 accumulators and outputs bit-exact (int32 split partials add
     exactly, so the split does not change results).
-Shapes cover every fragment count (M = 1..16 in 4-row fragments), N not a
+Shapes cover both fragment counts (M = 1..8 in 4-row fragments), N not a
 multiple of the 256-column tile, K with a partial last scale block and with
 chunks past K, and block_k down to one 32-row chunk.
 """
@@ -130,17 +132,17 @@ def test_skinny_w8a8_outputs_bitexact(out, modes, m, bias):
     assert np.array_equal(H.from_dev_f32(c), exp)
 
 
-def test_skinny_matches_tiled_boundary():
-    # M = 16 (skinny) and M = 17 (tiled) on the same data: the W8A8
-    # accumulators agree exactly; the fp8 outputs differ only by fp32
+def test_skinny_matches_split_boundary():
+    # M = 8 (skinny) and M = 9 (split-K 256x256 kernel) on the same data: the
+    # W8A8 accumulators agree exactly; the fp8 outputs differ only by fp32
     # association (32-row chunk promotion and split sums against 128-row block
-    # promotion), measured at ~1.4e-5 of max |out| for K = 2048.
-    rng = np.random.default_rng(1617)
+    # promotion; ~1.4e-5 of max |out| measured for K = 2048).
+    rng = np.random.default_rng(89)
     n, k = 512, 2048
-    a = rng.integers(-127, 128, (17, k)).astype(np.int8)
+    a = rng.integers(-127, 128, (9, k)).astype(np.int8)
     b = rng.integers(-127, 128, (k, n)).astype(np.int8)
-    assert np.array_equal(w8a8_acc_dev(a[:16], b), w8a8_acc_dev(a, b)[:16])
-    a8, b8, a_s, b_s = fp8_case(17, n, k, seed=17)
-    g17 = run_fp8(a8, b8, a_s, b_s, 128, 128, out="f32")
-    g16 = run_fp8(a8[:16].copy(), b8, a_s[:16].copy(), b_s, 128, 128, out="f32")
-    assert O.rel_err(g16, g17[:16]) <= 1e-4
+    assert np.array_equal(w8a8_acc_dev(a[:8], b), w8a8_acc_dev(a, b)[:8])
+    a8, b8, a_s, b_s = fp8_case(9, n, k, seed=9)
+    g9 = run_fp8(a8, b8, a_s, b_s, 128, 128, out="f32")
+    g8 = run_fp8(a8[:8].copy(), b8, a_s[:8].copy(), b_s, 128, 128, out="f32")
+    assert O.rel_err(g8, g9[:8]) <= 1e-4
