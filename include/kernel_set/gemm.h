@@ -1,10 +1,11 @@
 /*
  * kernel-set (MI355X build) -- quantized GEMMs.
  *
- * The four entry points keep the exact prototypes of the reference ABI
+ * The first four entry points keep the exact prototypes of the reference ABI
  * (include/kernel_set/gemm.h of cklxx/kernel-set) so existing bindings load
- * this library unchanged. All matrices are row-major and device resident;
- * every call only enqueues work on `stream` (NULL = null stream).
+ * this library unchanged; ks_gemm_fp8_blockwise_fused_quant is an extension
+ * of this build. All matrices are row-major and device resident; every call
+ * only enqueues work on `stream` (NULL = null stream).
  *
  * Out of scope for this build (not exported): ks_gemm, ks_gemm_bias_act,
  * ks_gemm_batched, ks_gemm_nvfp4.
@@ -65,6 +66,28 @@ KS_API ks_status_t ks_gemm_fp8_blockwise(void* out, const void* a_fp8,
                                          int block_k, ks_dtype_t fp8_dtype,
                                          ks_dtype_t out_dtype,
                                          ks_stream_t stream);
+
+/* Extension: no counterpart in the reference. For callers that hold bf16 /
+ * f16 / f32 activations and would otherwise call ks_quantize_fp8_group and
+ * then ks_gemm_fp8_blockwise (the reference's own 1 x 128 / 128 x 128 recipe,
+ * quant.h:35-40 + gemm.h:79-98). Defined as exactly that composition:
+ *   (a8, a_scale) = ks_quantize_fp8_group(a, group_size = block_k, fp8_dtype)
+ *   out           = ks_gemm_fp8_blockwise(a8, b_fp8, a_scale, b_scale, ...)
+ * and returns the same bits. For M <= 8 it runs as one pass (each workgroup
+ * quantizes its own K slice into LDS; requires block_k in {32, 64, 128, 256},
+ * block_n % 16 == 0, N % 16 == 0, K % 32 == 0 and a 16-byte-aligned `a`);
+ * otherwise it quantizes into library staging (per device and stream) and runs
+ * the GEMM. a_dtype f32/f16/bf16; fp8_dtype e4m3/e5m2; out_dtype f32/f16/bf16. */
+KS_API ks_status_t ks_gemm_fp8_blockwise_fused_quant(void* out, const void* a,
+                                                     const void* b_fp8,
+                                                     const float* b_scale,
+                                                     int64_t m, int64_t n,
+                                                     int64_t k, int block_n,
+                                                     int block_k,
+                                                     ks_dtype_t a_dtype,
+                                                     ks_dtype_t fp8_dtype,
+                                                     ks_dtype_t out_dtype,
+                                                     ks_stream_t stream);
 
 KS_END_EXTERN_C
 

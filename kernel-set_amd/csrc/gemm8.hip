@@ -20,6 +20,7 @@
 // W8A8 (gemm_w8a8.cu:120-142): exact int32 accumulation over all of K, then
 // v = (float(acc) * a_s) * b_s (+ bias), with no contraction of the multiplies.
 #include "kernel_set/gemm.h"
+#include "kernel_set/quant.h"
 #include "kernel_set/testing.h"
 #include "ks_common.hpp"
 #include "gemm8_common.hpp"
@@ -764,7 +765,7 @@ inline bool skinny_ok(const Args& p) {
          (reinterpret_cast<uintptr_t>(p.a) & 7u) == 0 && (reinterpret_cast<uintptr_t>(p.b) & 15u) == 0;
 }
 
-template <int KIND, typename Out, int MB, int CH>
+template <int KIND, typename Out, int MB, int CH, typename In = void>
 ks_status_t launch_skinny(Args p, hipStream_t s, const char* who) {
   const int64_t tiles = (p.n + skinny::kTileN - 1) / skinny::kTileN;
   const int64_t kwg = static_cast<int64_t>(skinny::kWaves) * CH * skinny::kChunk;
@@ -773,7 +774,7 @@ ks_status_t launch_skinny(Args p, hipStream_t s, const char* who) {
   ks_status_t st = get_scratch(s, static_cast<size_t>(p.splits) * p.m * p.n, 0, &sc, who);
   if (st != KS_SUCCESS) return st;
   p.ws = sc.partial;
-  hipLaunchKernelGGL((skinny::skinny_kernel<KIND, MB, CH>), dim3(static_cast<unsigned>(tiles * p.splits)),
+  hipLaunchKernelGGL((skinny::skinny_kernel<KIND, MB, CH, In>), dim3(static_cast<unsigned>(tiles * p.splits)),
                      dim3(skinny::kThreads), 0, s, p);
   hipLaunchKernelGGL((skinny::skinny_reduce_kernel<KIND, Out>),
                      dim3(static_cast<unsigned>((p.m * p.n + 255) / 256)), dim3(256), 0, s, p);
@@ -784,22 +785,42 @@ ks_status_t launch_skinny(Args p, hipStream_t s, const char* who) {
 // Measured on MI355X (graph replay, N = K = 7168, fp8 blockwise): M = 1/4/8
 // 13.7/13.6/15.1 us with 4 chunks against 13.9/14.2/18.0 with 2; at
 // N = K = 4096 only one chunk per wave fills the chip.
-template <int KIND, typename Out, int MB>
+template <int KIND, typename Out, int MB, typename In = void>
 ks_status_t skinny_chunks(const Args& p, hipStream_t s, const char* who) {
   const int64_t tiles = (p.n + skinny::kTileN - 1) / skinny::kTileN;
   auto wgs = [&](int ch) {
     const int64_t kwg = int64_t{ch} * skinny::kWaves * skinny::kChunk;
     return tiles * ((p.k + kwg - 1) / kwg);
   };
-  if (wgs(4) >= 192) return launch_skinny<KIND, Out, MB, 4>(p, s, who);
-  if (wgs(2) >= 192) return launch_skinny<KIND, Out, MB, 2>(p, s, who);
-  return launch_skinny<KIND, Out, MB, 1>(p, s, who);
+  if (wgs(4) >= 192) return launch_skinny<KIND, Out, MB, 4, In>(p, s, who);
+  if (wgs(2) >= 192) return launch_skinny<KIND, Out, MB, 2, In>(p, s, who);
+  return launch_skinny<KIND, Out, MB, 1, In>(p, s, who);
 }
 
-template <int KIND, typename Out>
+template <int KIND, typename Out, typename In = void>
 ks_status_t run_skinny(const Args& p, hipStream_t s, const char* who) {
-  if (p.m <= 4) return skinny_chunks<KIND, Out, 1>(p, s, who);
-  return skinny_chunks<KIND, Out, 2>(p, s, who);
+  if (p.m <= 4) return skinny_chunks<KIND, Out, 1, In>(p, s, who);
+  return skinny_chunks<KIND, Out, 2, In>(p, s, who);
+}
+
+// Fused quantize + blockwise GEMM at decode shapes: by output and input type.
+template <int KIND, typename In>
+ks_status_t run_fused_in(const Args& p, ks_dtype_t out_dtype, hipStream_t s, const char* who) {
+  switch (out_dtype) {
+    case KS_DTYPE_F32: return run_skinny<KIND, f32_t, In>(p, s, who);
+    case KS_DTYPE_F16: return run_skinny<KIND, f16_t, In>(p, s, who);
+    default: return run_skinny<KIND, bf16_t, In>(p, s, who);
+  }
+}
+
+template <int KIND>
+ks_status_t run_fused(const Args& p, ks_dtype_t a_dtype, ks_dtype_t out_dtype, hipStream_t s,
+                      const char* who) {
+  switch (a_dtype) {
+    case KS_DTYPE_F32: return run_fused_in<KIND, f32_t>(p, out_dtype, s, who);
+    case KS_DTYPE_F16: return run_fused_in<KIND, f16_t>(p, out_dtype, s, who);
+    default: return run_fused_in<KIND, bf16_t>(p, out_dtype, s, who);
+  }
 }
 
 template <int KIND>
@@ -914,6 +935,64 @@ ks_status_t ks_gemm_fp8_blockwise(void* out, const void* a_fp8, const void* b_fp
   if (st != KS_SUCCESS) return st;
   KS_LAUNCH_STATUS("ks_gemm_fp8_blockwise");
   return KS_SUCCESS;
+}
+
+ks_status_t ks_gemm_fp8_blockwise_fused_quant(void* out, const void* a, const void* b_fp8,
+                                              const float* b_scale, int64_t m, int64_t n,
+                                              int64_t k, int block_n, int block_k,
+                                              ks_dtype_t a_dtype, ks_dtype_t fp8_dtype,
+                                              ks_dtype_t out_dtype, ks_stream_t stream) {
+  static const char* who = "ks_gemm_fp8_blockwise_fused_quant";
+  KS_REQUIRE_PTR(out);
+  KS_REQUIRE_PTR(a);
+  KS_REQUIRE_PTR(b_fp8);
+  KS_REQUIRE_PTR(b_scale);
+  if (m <= 0 || n <= 0 || k <= 0) KS_FAIL(KS_ERROR_INVALID_ARGUMENT, "ks_gemm_fp8_blockwise_fused_quant: bad shape");
+  if (block_n <= 0 || block_k <= 0)
+    KS_FAIL(KS_ERROR_INVALID_ARGUMENT, "ks_gemm_fp8_blockwise_fused_quant: block_n/block_k must be > 0");
+  if (a_dtype != KS_DTYPE_F32 && a_dtype != KS_DTYPE_F16 && a_dtype != KS_DTYPE_BF16)
+    KS_FAIL(KS_ERROR_UNSUPPORTED_DTYPE, "ks_gemm_fp8_blockwise_fused_quant: a_dtype must be f32/f16/bf16");
+  if (fp8_dtype != KS_DTYPE_F8E4M3 && fp8_dtype != KS_DTYPE_F8E5M2)
+    KS_FAIL(KS_ERROR_UNSUPPORTED_DTYPE, "ks_gemm_fp8_blockwise_fused_quant: fp8_dtype must be e4m3 or e5m2");
+  if (out_dtype != KS_DTYPE_F32 && out_dtype != KS_DTYPE_F16 && out_dtype != KS_DTYPE_BF16)
+    KS_FAIL(KS_ERROR_UNSUPPORTED_DTYPE, "ks_gemm_fp8_blockwise_fused_quant: out_dtype must be f32/f16/bf16");
+  if (mul_overflows(m, k) || mul_overflows(k, n) || mul_overflows(m, n))
+    KS_FAIL(KS_ERROR_UNSUPPORTED_SHAPE, "ks_gemm_fp8_blockwise_fused_quant: M*K / K*N / M*N exceeds int64 range");
+  Args p{};
+  p.out = out;
+  p.a_in = a;
+  p.b = static_cast<const uint8_t*>(b_fp8);
+  p.b_scale = b_scale;
+  p.m = m; p.n = n; p.k = k;
+  p.block_n = block_n; p.block_k = block_k;
+  p.nkb = (k + block_k - 1) / block_k;
+  p.nnb = (n + block_n - 1) / block_n;
+  auto s = to_stream(stream);
+  // One pass at decode shapes: the skinny kernel quantizes its own slice.
+  // Its checks see the activation pointer as operand A (16-byte aligned rows).
+  Args q = p;
+  q.a = static_cast<const uint8_t*>(a);
+  const bool gs_ok = block_k == 32 || block_k == 64 || block_k == 128 || block_k == 256;
+  if (skinny_ok(q) && gs_ok && block_n % 16 == 0 && (reinterpret_cast<uintptr_t>(a) & 15u) == 0) {
+    const ks_status_t st = fp8_dtype == KS_DTYPE_F8E4M3
+        ? run_fused<FP8_E4M3>(p, a_dtype, out_dtype, s, who)
+        : run_fused<FP8_E5M2>(p, a_dtype, out_dtype, s, who);
+    if (st != KS_SUCCESS) return st;
+    KS_LAUNCH_STATUS("ks_gemm_fp8_blockwise_fused_quant");
+    return KS_SUCCESS;
+  }
+  // Otherwise the per-token-group quantizer writes codes and scales to library
+  // staging and the blockwise GEMM reads them (same stream, so ordered).
+  const size_t codes = static_cast<size_t>((m * k + 255) / 256 * 256);
+  Scratch sc;
+  ks_status_t st = get_scratch(s, 0, codes + static_cast<size_t>(m * p.nkb) * sizeof(float), &sc, who);
+  if (st != KS_SUCCESS) return st;
+  uint8_t* a8 = static_cast<uint8_t*>(sc.staging);
+  float* a_s = reinterpret_cast<float*>(a8 + codes);
+  st = ks_quantize_fp8_group(a8, a_s, a, m, k, block_k, a_dtype, fp8_dtype, stream);
+  if (st != KS_SUCCESS) return st;
+  return ks_gemm_fp8_blockwise(out, a8, b_fp8, a_s, b_scale, m, n, k, block_n, block_k, fp8_dtype,
+                               out_dtype, stream);
 }
 
 ks_status_t ks_gemm_fp8(void* out, const void* a_fp8, const void* b_fp8, const float* a_scale,

@@ -39,6 +39,7 @@ struct Args {
   int a_per_token, b_per_channel;  // w8a8
   int splits;                      // skinny path: K splits
   void* ws;                        // skinny path: split partial plane
+  const void* a_in;                // fused quantize + GEMM: unquantized activations [M, K]
 };
 
 }  // namespace gemm8

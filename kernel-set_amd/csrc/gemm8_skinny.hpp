@@ -35,6 +35,8 @@
 // whole block; per-chunk promotion changes only fp32 rounding.
 #pragma once
 
+#include <type_traits>
+
 #include "gemm8_common.hpp"
 
 namespace ks {
@@ -56,16 +58,54 @@ __device__ inline void map_tile(int bid, int nblocks, int splits, int* tile, int
   *split = logical % splits;
 }
 
+// Unquantized activations of the fused path: 8 consecutive elements as raw
+// words (plain loads: every column tile's workgroups re-read these rows), and
+// their conversion to fp32, kept apart so the conversion does not make the
+// compiler wait on the load before the B stream is issued.
+template <typename In>
+__device__ inline void load8_act_raw(const typename In::storage* p, uint4 w[2]) {
+  w[0] = *reinterpret_cast<const uint4*>(p);
+  if constexpr (std::is_same<In, f32_t>::value) w[1] = *reinterpret_cast<const uint4*>(p + 4);
+}
+
+template <typename In>
+__device__ inline void act_to_f32(const uint4 w[2], float v[8]) {
+  if constexpr (std::is_same<In, f32_t>::value) {
+    const uint32_t d[8] = {w[0].x, w[0].y, w[0].z, w[0].w, w[1].x, w[1].y, w[1].z, w[1].w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = __uint_as_float(d[i]);
+  } else {
+    const uint32_t d[4] = {w[0].x, w[0].y, w[0].z, w[0].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = elem<In>::to_f32(static_cast<uint16_t>(d[i] & 0xffffu));
+      v[2 * i + 1] = elem<In>::to_f32(static_cast<uint16_t>(d[i] >> 16));
+    }
+  }
+}
+
 // Requirements (checked by the host): m <= 4*MB, n % 16 == 0, k % 32 == 0,
 // a 8-byte and b 16-byte aligned, M*K, K*N and splits*M*N below 2^31;
 // blockwise: block_k % 32 == 0, block_n % 16 == 0.
-template <int KIND, int MB, int CH>
+//
+// In != void: fused activation quantization (fp8 blockwise kinds only). The
+// workgroup quantizes its own slice A_in[0:M, kwg0 : kwg0 + 256*CH] into LDS
+// in 1 x block_k groups (block_k in {32, 64, 128, 256}, so the slice holds
+// whole groups) with the standalone quantizer's arithmetic (scale_from_amax,
+// enc8), then reads A codes and scales from LDS. Its activation loads are
+// issued before the B stream, so B stays in flight while it quantizes.
+template <int KIND, int MB, int CH, typename In = void>
 __global__ void __launch_bounds__(kThreads)
 skinny_kernel(Args p) {
   constexpr bool kInt = KIND == INT8 || KIND == INT8_RAW;
   constexpr bool kBlock = is_fp8_block(KIND);
+  constexpr bool kFused = !std::is_void<In>::value;
+  static_assert(!kFused || kBlock, "fused quantization serves the fp8 blockwise kinds");
   constexpr int kRows = 4 * MB;
+  constexpr int kSliceK = kWaves * CH * kChunk;  // k-rows per workgroup
   __shared__ uint32_t red[kWaves / 2][kRows][kTileN];
+  __shared__ __attribute__((aligned(16))) uint8_t sa[kFused ? kRows : 1][kFused ? kSliceK : 16];
+  __shared__ float ss[kFused ? kRows : 1][kFused ? kSliceK / 32 : 1];
 
   int tile, split;
   map_tile(blockIdx.x, gridDim.x, p.splits, &tile, &split);
@@ -75,31 +115,56 @@ skinny_kernel(Args p) {
   const int m = static_cast<int>(p.m), n = static_cast<int>(p.n), k = static_cast<int>(p.k);
   const int col = tile * kTileN + 16 * li;
   const int colc = col < n ? col : n - 16;  // lanes past N load a valid line, store nothing
-  const int kw = (split * kWaves + wave) * CH * kChunk;
+  const int kwg0 = split * kSliceK;
+  const int kw = kwg0 + wave * CH * kChunk;
 
-  // Activation bytes first (8 per lane per fragment and chunk, L2-resident),
-  // then all of the wave's B bytes (CH * 8 x 16 B per lane): loads complete in
-  // order, so chunk c's math waits only for chunk c's B rows.
-  uint2 av[CH][MB];
+  // Fused: this workgroup's activation slice, 8 elements per slot, issued first.
+  constexpr int kPieces = kSliceK / 8;            // 8-element pieces per row
+  constexpr int kSlots = kRows * kPieces;
+  constexpr int kU = kFused ? (kSlots + kThreads - 1) / kThreads : 1;
+  uint4 xr[kU][2];
+  bool xlive[kU];
+  if constexpr (kFused) {
+    using S = typename In::storage;
 #pragma unroll
-  for (int c = 0; c < CH; ++c)
-#pragma unroll
-    for (int f = 0; f < MB; ++f) {
-      const int am = min(4 * f + li / 4, m - 1);
-      const int ka = min(kw + kChunk * c, k - kChunk) + 8 * g;
-      av[c][f] = *reinterpret_cast<const uint2*>(p.a + static_cast<int64_t>(am) * k + ka);
+    for (int u = 0; u < kU; ++u) {
+      const int slot = threadIdx.x + u * kThreads;
+      const int row = slot / kPieces, kc = kwg0 + 8 * (slot % kPieces);
+      xlive[u] = slot < kSlots && row < m && kc < k;
+      const int64_t off = xlive[u] ? static_cast<int64_t>(row) * k + kc : 0;
+      load8_act_raw<In>(static_cast<const S*>(p.a_in) + off, xr[u]);
     }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // Pre-quantized: activation bytes (8 per lane per fragment and chunk,
+  // L2-resident) and scales first, then all of the wave's B bytes (CH * 8 x
+  // 16 B per lane): loads complete in order, so chunk c's math waits only for
+  // chunk c's B rows.
+  uint2 av[CH][MB];
+  float bsc[CH], asc[CH][MB];
+  if constexpr (!kFused) {
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+#pragma unroll
+      for (int f = 0; f < MB; ++f) {
+        const int am = min(4 * f + li / 4, m - 1);
+        const int ka = min(kw + kChunk * c, k - kChunk) + 8 * g;
+        av[c][f] = *reinterpret_cast<const uint2*>(p.a + static_cast<int64_t>(am) * k + ka);
+      }
+  }
   // Scales of each chunk's block (blockwise): b_scale per lane column group,
   // a_scale per output row 4f + g of the lane.
-  float bsc[CH], asc[CH][MB];
-  if constexpr (is_fp8_block(KIND)) {
+  if constexpr (kBlock) {
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
       const int kb = min(kw + kChunk * c, k - kChunk) / p.block_k;
       bsc[c] = p.b_scale[static_cast<int64_t>(kb) * p.nnb + colc / p.block_n];
+      if constexpr (!kFused) {
 #pragma unroll
-      for (int f = 0; f < MB; ++f)
-        asc[c][f] = p.a_scale[static_cast<int64_t>(min(4 * f + g, m - 1)) * p.nkb + kb];
+        for (int f = 0; f < MB; ++f)
+          asc[c][f] = p.a_scale[static_cast<int64_t>(min(4 * f + g, m - 1)) * p.nkb + kb];
+      }
     }
   }
   uint4 bv[CH][8];
@@ -113,6 +178,40 @@ skinny_kernel(Args p) {
   // Keep every load above the math: the scheduler would otherwise sink later
   // chunks' loads below earlier chunks' MFMAs and serialize their latency.
   __builtin_amdgcn_sched_barrier(0);
+
+  if constexpr (kFused) {
+    // 1 x block_k groups of G = block_k / 8 consecutive lanes (G divides 64
+    // and the slice width, so a group never straddles a wave or a row).
+    using Enc = typename std::conditional<fp8_fmt(KIND) == 1, e5m2_t, e4m3_t>::type;
+    const int gl = p.block_k / 8;
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int slot = threadIdx.x + u * kThreads;
+      const int row = slot / kPieces, pc = slot % kPieces;
+      float xv[8];
+      act_to_f32<In>(xr[u], xv);
+      float amax = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) amax = fmaxf(amax, xlive[u] ? fabsf(xv[i]) : 0.f);
+      amax = group_max(amax, gl);
+      const float sc = scale_from_amax<Enc>(amax);
+      const uint2 code = enc8<Enc>::run(xv, 1.0f / sc);
+      if (slot < kSlots) {
+        *reinterpret_cast<uint2*>(&sa[row][8 * pc]) = code;
+        if (pc % gl == 0) ss[row][pc / gl] = sc;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int kl = min(kw + kChunk * c, k - kChunk) - kwg0;  // chunk start in the slice
+#pragma unroll
+      for (int f = 0; f < MB; ++f) {
+        av[c][f] = *reinterpret_cast<const uint2*>(&sa[4 * f + li / 4][kl + 8 * g]);
+        asc[c][f] = ss[4 * f + g][kl / p.block_k];
+      }
+    }
+  }
 
   // A operand selectors: byte r of the lane's 8 activation bytes goes to byte
   // li % 4 of dword r, the other bytes are zero (v_perm selector 0x0c).

@@ -224,6 +224,45 @@ struct e5m2_t {
 constexpr float kEpsScale = 1e-12f;  // floor of every dynamic scale
 constexpr float kInt8Max = 127.0f;
 
+// Dynamic quantization scale of a group/row/tensor with max |x| = amax
+// (quant_fp8_group.cu:94-106 of cklxx/kernel-set): IEEE-correct fp32 divide,
+// floored at kEpsScale. Codes are then enc(x * (1.0f / scale)).
+template <typename Enc>
+__device__ inline float scale_from_amax(float amax) {
+  return fmaxf(amax / Enc::qmax, kEpsScale);
+}
+
+// Eight scaled values -> eight fp8 codes (two dwords, element i in byte i % 4
+// of dword i / 4). fp8 codes come from the hardware converters
+// (v_cvt_pk_fp8_f32 / v_cvt_pk_bf8_f32, round to nearest even): every value
+// they see is x * (1/s) with s >= amax/qmax, so |x/s| <= qmax(1 + 2^-23) and
+// the saturating and non-saturating conversions give the same code.
+template <typename Enc>
+struct enc8;  // specialized per code type (int8 in quant.hip)
+
+template <>
+struct enc8<e4m3_t> {
+  __device__ static inline uint2 run(const float v[8], float inv) {
+    int lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[0] * inv, v[1] * inv, 0, false);
+    lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[2] * inv, v[3] * inv, lo, true);
+    int hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[4] * inv, v[5] * inv, 0, false);
+    hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[6] * inv, v[7] * inv, hi, true);
+    return make_uint2(static_cast<uint32_t>(lo), static_cast<uint32_t>(hi));
+  }
+};
+
+template <>
+struct enc8<e5m2_t> {
+  __device__ static inline uint2 run(const float v[8], float inv) {
+    int lo = __builtin_amdgcn_cvt_pk_bf8_f32(v[0] * inv, v[1] * inv, 0, false);
+    lo = __builtin_amdgcn_cvt_pk_bf8_f32(v[2] * inv, v[3] * inv, lo, true);
+    int hi = __builtin_amdgcn_cvt_pk_bf8_f32(v[4] * inv, v[5] * inv, 0, false);
+    hi = __builtin_amdgcn_cvt_pk_bf8_f32(v[6] * inv, v[7] * inv, hi, true);
+    return make_uint2(static_cast<uint32_t>(lo), static_cast<uint32_t>(hi));
+  }
+};
+
+
 // ---------------------------------------------------------------------------
 // wave64 reductions (xor butterflies over all 64 lanes)
 // ---------------------------------------------------------------------------

@@ -68,10 +68,6 @@ struct i8_t {
   }
 };
 
-template <typename Enc>
-__device__ inline float scale_from_amax(float amax) {
-  return fmaxf(amax / Enc::qmax, kEpsScale);
-}
 
 template <typename Enc>
 __device__ inline void store8(uint8_t* dst, const float v[8], float inv) {
@@ -97,43 +93,23 @@ __device__ inline void store8(uint8_t* dst, const float v[8], float inv) {
 // and the non-saturating conversion give the same code. Index math is 32-bit
 // when the tensor allows it (Idx = uint32_t), with L a compile-time power of 2.
 // ===========================================================================
-template <typename Enc>
-struct enc8;
+// enc8<e4m3_t> / enc8<e5m2_t> (hardware converters) live in ks_common.hpp.
+}  // namespace quant
 
 template <>
-struct enc8<e4m3_t> {
-  __device__ static inline uint2 run(const float v[8], float inv) {
-    int lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[0] * inv, v[1] * inv, 0, false);
-    lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[2] * inv, v[3] * inv, lo, true);
-    int hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[4] * inv, v[5] * inv, 0, false);
-    hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[6] * inv, v[7] * inv, hi, true);
-    return make_uint2(static_cast<uint32_t>(lo), static_cast<uint32_t>(hi));
-  }
-};
-
-template <>
-struct enc8<e5m2_t> {
-  __device__ static inline uint2 run(const float v[8], float inv) {
-    int lo = __builtin_amdgcn_cvt_pk_bf8_f32(v[0] * inv, v[1] * inv, 0, false);
-    lo = __builtin_amdgcn_cvt_pk_bf8_f32(v[2] * inv, v[3] * inv, lo, true);
-    int hi = __builtin_amdgcn_cvt_pk_bf8_f32(v[4] * inv, v[5] * inv, 0, false);
-    hi = __builtin_amdgcn_cvt_pk_bf8_f32(v[6] * inv, v[7] * inv, hi, true);
-    return make_uint2(static_cast<uint32_t>(lo), static_cast<uint32_t>(hi));
-  }
-};
-
-template <>
-struct enc8<i8_t> {
+struct enc8<quant::i8_t> {
   __device__ static inline uint2 run(const float v[8], float inv) {
     uint32_t lo = 0, hi = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      lo |= static_cast<uint32_t>(i8_t::enc(v[i] * inv)) << (8 * i);
-      hi |= static_cast<uint32_t>(i8_t::enc(v[i + 4] * inv)) << (8 * i);
+      lo |= static_cast<uint32_t>(quant::i8_t::enc(v[i] * inv)) << (8 * i);
+      hi |= static_cast<uint32_t>(quant::i8_t::enc(v[i + 4] * inv)) << (8 * i);
     }
     return make_uint2(lo, hi);
   }
 };
+
+namespace quant {
 
 constexpr int kGroupUnroll = 1;  // slots per thread (2 and 4 measured slower)
 constexpr unsigned kLoopBlocks = 2048;  // persistent grid of the per-block quantizer

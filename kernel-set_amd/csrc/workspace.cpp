@@ -14,8 +14,8 @@ namespace {
 struct Entry {
   float* partial = nullptr;
   size_t partial_cap = 0;
-  unsigned* counters = nullptr;
-  size_t counter_cap = 0;
+  void* staging = nullptr;
+  size_t staging_cap = 0;
 };
 
 std::mutex g_mu;
@@ -25,7 +25,7 @@ size_t round_up(size_t v, size_t q) { return (v + q - 1) / q * q; }
 
 }  // namespace
 
-ks_status_t get_scratch(hipStream_t stream, size_t partial_floats, size_t counters,
+ks_status_t get_scratch(hipStream_t stream, size_t partial_floats, size_t staging_bytes,
                         Scratch* out, const char* who) {
   int dev = 0;
   ks_status_t st = check_hip(hipGetDevice(&dev), who);
@@ -49,26 +49,24 @@ ks_status_t get_scratch(hipStream_t stream, size_t partial_floats, size_t counte
     }
     e.partial_cap = cap;
   }
-  if (counters > e.counter_cap) {
-    if (e.counters) {
+  if (staging_bytes > e.staging_cap) {
+    if (e.staging) {
       st = check_hip(hipStreamSynchronize(stream), who);
       if (st != KS_SUCCESS) return st;
-      (void)hipFree(e.counters);
-      e.counters = nullptr;
-      e.counter_cap = 0;
+      (void)hipFree(e.staging);
+      e.staging = nullptr;
+      e.staging_cap = 0;
     }
-    const size_t cap = round_up(counters, 4096);
-    if (hipMalloc(&e.counters, cap * sizeof(unsigned)) != hipSuccess) {
-      e.counters = nullptr;
-      set_last_error(std::string(who) + ": counter allocation failed");
+    const size_t cap = round_up(staging_bytes, size_t{1} << 20);
+    if (hipMalloc(&e.staging, cap) != hipSuccess) {
+      e.staging = nullptr;
+      set_last_error(std::string(who) + ": staging allocation failed");
       return KS_ERROR_OUT_OF_MEMORY;
     }
-    st = check_hip(hipMemset(e.counters, 0, cap * sizeof(unsigned)), who);
-    if (st != KS_SUCCESS) return st;
-    e.counter_cap = cap;
+    e.staging_cap = cap;
   }
   out->partial = e.partial;
-  out->counters = e.counters;
+  out->staging = e.staging;
   return KS_SUCCESS;
 }
 

@@ -93,3 +93,23 @@ def gemm_fp8_blockwise(out: TensorLike, a_fp8: TensorLike, b_fp8: TensorLike,
         default_stream(stream, out if not isinstance(out, int) else a_fp8)),
         "ks_gemm_fp8_blockwise")
     return out
+
+
+def gemm_fp8_blockwise_fused_quant(out: TensorLike, a: TensorLike, b_fp8: TensorLike,
+                                   b_scale: TensorLike, m: int, n: int, k: int,
+                                   block_n: int = 128, block_k: int = 128,
+                                   a_dtype: int = None, fp8_dtype: int = None,
+                                   out_dtype: int = None, stream: TensorLike = None) -> TensorLike:
+    """Extension (no reference counterpart): ``out = gemm_fp8_blockwise(
+    quantize_fp8_group(a, group_size=block_k, fp8_dtype), b_fp8, b_scale)``
+    with the same bits as that two-call sequence. ``a`` is bf16/f16/f32
+    ``[M, K]``; decode shapes (M <= 8) run as a single pass."""
+    adt = infer_dtype(a, a_dtype)
+    fdt = infer_dtype(b_fp8, fp8_dtype)
+    odt = _out_dtype(out, out_dtype, "ks_gemm_fp8_blockwise_fused_quant")
+    check(lib.ks_gemm_fp8_blockwise_fused_quant(
+        ptr(out, name="out"), ptr(a, name="a"), ptr(b_fp8, name="b_fp8"),
+        _f32(b_scale, name="b_scale"), int(m), int(n), int(k), int(block_n), int(block_k),
+        adt, fdt, odt, default_stream(stream, out if not isinstance(out, int) else a)),
+        "ks_gemm_fp8_blockwise_fused_quant")
+    return out

@@ -124,6 +124,25 @@ def test_fp8_gemm_validation():
              DType.F8E5M2, DType.I8, None) == Status.ERROR_UNSUPPORTED_DTYPE
 
 
+def test_fp8_blockwise_fused_quant_validation():
+    # extension entry point: pointers, shape, blocks, then the three dtypes
+    f = _lib.lib.ks_gemm_fp8_blockwise_fused_quant
+    fp = ctypes.cast(P, _lib._F32P)
+    ok = (DType.BF16, DType.F8E4M3, DType.BF16, None)
+    assert f(P, P, P, None, 1, 1, 1, 128, 128, *ok) == Status.ERROR_INVALID_ARGUMENT
+    assert ks.last_error_string() == "null arg: b_scale"
+    assert f(P, P, P, fp, 1, 0, 1, 128, 128, *ok) == Status.ERROR_INVALID_ARGUMENT
+    assert f(P, P, P, fp, 1, 1, 1, 128, 0, *ok) == Status.ERROR_INVALID_ARGUMENT
+    assert f(P, P, P, fp, 1, 1, 1, 128, 128, DType.I8, DType.F8E4M3, DType.BF16, None) \
+        == Status.ERROR_UNSUPPORTED_DTYPE
+    assert f(P, P, P, fp, 1, 1, 1, 128, 128, DType.BF16, DType.BF16, DType.BF16, None) \
+        == Status.ERROR_UNSUPPORTED_DTYPE
+    assert f(P, P, P, fp, 1, 1, 1, 128, 128, DType.BF16, DType.F8E5M2, DType.I8, None) \
+        == Status.ERROR_UNSUPPORTED_DTYPE
+    big = 1 << 40
+    assert f(P, P, P, fp, big, big, 8, 128, 128, *ok) == Status.ERROR_UNSUPPORTED_SHAPE
+
+
 def test_fp8_blockwise_validation():
     f = _lib.lib.ks_gemm_fp8_blockwise
     fp = ctypes.cast(P, _lib._F32P)
