@@ -756,13 +756,15 @@ inline unsigned simple_grid(const Args& p) {
 
 // Decode shapes (M <= 8) take the skinny kernel: B streamed once, K split
 // over enough workgroups to fill the chip, partials reduced in split order.
-// From M = 9 the split-K 256x256 kernel is faster (N = K = 7168: M = 16
-// 23.5 us skinny against 22.4 us split-K at M = 17).
+// From M = 9 the split-K 256x256 kernel is as fast: four row fragments need
+// ~168 VGPRs, so a CU holds one 8-wave workgroup (half the bytes in flight of
+// M <= 8) and the grid runs in 1.5 rounds (N = K = 7168: M = 9..16 21.6-23.6
+// us skinny against 23.0 us split-K at M = 17).
 inline bool skinny_ok(const Args& p) {
   return p.m <= skinny::kMaxM && p.n % 16 == 0 && p.k % skinny::kChunk == 0 &&
          p.m * p.k < (int64_t{1} << 31) && p.k * p.n < (int64_t{1} << 31) &&
          (p.k / skinny::kChunk) * p.m * p.n < (int64_t{1} << 31) &&
-         (reinterpret_cast<uintptr_t>(p.a) & 7u) == 0 && (reinterpret_cast<uintptr_t>(p.b) & 15u) == 0;
+         (reinterpret_cast<uintptr_t>(p.a) & 15u) == 0 && (reinterpret_cast<uintptr_t>(p.b) & 15u) == 0;
 }
 
 template <int KIND, typename Out, int MB, int CH, typename In = void>

@@ -85,7 +85,7 @@ __device__ inline void act_to_f32(const uint4 w[2], float v[8]) {
 }
 
 // Requirements (checked by the host): m <= 4*MB, n % 16 == 0, k % 32 == 0,
-// a 8-byte and b 16-byte aligned, M*K, K*N and splits*M*N below 2^31;
+// a and b 16-byte aligned, M*K, K*N and splits*M*N below 2^31;
 // blockwise: block_k % 32 == 0, block_n % 16 == 0.
 //
 // In != void: fused activation quantization (fp8 blockwise kinds only). The
@@ -104,8 +104,13 @@ skinny_kernel(Args p) {
   constexpr int kRows = 4 * MB;
   constexpr int kSliceK = kWaves * CH * kChunk;  // k-rows per workgroup
   __shared__ uint32_t red[kWaves / 2][kRows][kTileN];
-  __shared__ __attribute__((aligned(16))) uint8_t sa[kFused ? kRows : 1][kFused ? kSliceK : 16];
-  __shared__ float ss[kFused ? kRows : 1][kFused ? kSliceK / 32 : 1];
+  // The workgroup's activation slice (codes, or the fused path's quantized
+  // values) and its a_scale entries, staged through LDS: a few 16-byte loads
+  // per thread issued before the B stream, rather than per-fragment 8-byte
+  // loads that the compiler may serialize under register pressure.
+  constexpr int kSB = kSliceK / kChunk + 1;  // scale blocks a slice can touch
+  __shared__ __attribute__((aligned(16))) uint8_t sa[kRows][kSliceK];
+  __shared__ float ss[kRows][kSB];
 
   int tile, split;
   map_tile(blockIdx.x, gridDim.x, p.splits, &tile, &split);
@@ -117,13 +122,22 @@ skinny_kernel(Args p) {
   const int colc = col < n ? col : n - 16;  // lanes past N load a valid line, store nothing
   const int kwg0 = split * kSliceK;
   const int kw = kwg0 + wave * CH * kChunk;
+  const int kb0 = kBlock ? kwg0 / p.block_k : 0;  // first scale block of the slice
 
-  // Fused: this workgroup's activation slice, 8 elements per slot, issued first.
+  // ---- loads, in issue order: activation slice, scales, then B ----
+  // Fused: unquantized activations, 8 elements per slot.
   constexpr int kPieces = kSliceK / 8;            // 8-element pieces per row
   constexpr int kSlots = kRows * kPieces;
   constexpr int kU = kFused ? (kSlots + kThreads - 1) / kThreads : 1;
   uint4 xr[kU][2];
   bool xlive[kU];
+  // Pre-quantized: codes, 16 bytes per slot (rows and columns clamped; rows
+  // past M and chunks past K are masked out of the math).
+  constexpr int kAPieces = kRows * kSliceK / 16;
+  constexpr int kUA = kFused ? 1 : (kAPieces + kThreads - 1) / kThreads;
+  uint4 araw[kUA];
+  constexpr int kUS = (kRows * kSB + kThreads - 1) / kThreads;
+  float sraw[kUS];
   if constexpr (kFused) {
     using S = typename In::storage;
 #pragma unroll
@@ -134,39 +148,36 @@ skinny_kernel(Args p) {
       const int64_t off = xlive[u] ? static_cast<int64_t>(row) * k + kc : 0;
       load8_act_raw<In>(static_cast<const S*>(p.a_in) + off, xr[u]);
     }
-    __builtin_amdgcn_sched_barrier(0);
+  } else {
+#pragma unroll
+    for (int u = 0; u < kUA; ++u) {
+      const int piece = threadIdx.x + u * kThreads;
+      const int row = min(piece / (kSliceK / 16), m - 1);
+      const int kc = min(kwg0 + 16 * (piece % (kSliceK / 16)), k - 16);
+      araw[u] = *reinterpret_cast<const uint4*>(p.a + static_cast<int64_t>(row) * k + kc);
+    }
+    if constexpr (kBlock) {
+#pragma unroll
+      for (int u = 0; u < kUS; ++u) {
+        const int e = threadIdx.x + u * kThreads;
+        const int row = min(e / kSB, m - 1);
+        const int kb = min(kb0 + e % kSB, static_cast<int>(p.nkb) - 1);
+        sraw[u] = p.a_scale[static_cast<int64_t>(row) * p.nkb + kb];
+      }
+    }
   }
-
-  // Pre-quantized: activation bytes (8 per lane per fragment and chunk,
-  // L2-resident) and scales first, then all of the wave's B bytes (CH * 8 x
-  // 16 B per lane): loads complete in order, so chunk c's math waits only for
-  // chunk c's B rows.
   uint2 av[CH][MB];
   float bsc[CH], asc[CH][MB];
-  if constexpr (!kFused) {
-#pragma unroll
-    for (int c = 0; c < CH; ++c)
-#pragma unroll
-      for (int f = 0; f < MB; ++f) {
-        const int am = min(4 * f + li / 4, m - 1);
-        const int ka = min(kw + kChunk * c, k - kChunk) + 8 * g;
-        av[c][f] = *reinterpret_cast<const uint2*>(p.a + static_cast<int64_t>(am) * k + ka);
-      }
-  }
-  // Scales of each chunk's block (blockwise): b_scale per lane column group,
-  // a_scale per output row 4f + g of the lane.
+  // b_scale of each chunk's block, per lane column group.
   if constexpr (kBlock) {
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
       const int kb = min(kw + kChunk * c, k - kChunk) / p.block_k;
       bsc[c] = p.b_scale[static_cast<int64_t>(kb) * p.nnb + colc / p.block_n];
-      if constexpr (!kFused) {
-#pragma unroll
-        for (int f = 0; f < MB; ++f)
-          asc[c][f] = p.a_scale[static_cast<int64_t>(min(4 * f + g, m - 1)) * p.nkb + kb];
-      }
     }
   }
+  __builtin_amdgcn_sched_barrier(0);
+  // All of the wave's B bytes (CH * 8 x 16 B per lane), non-temporal.
   uint4 bv[CH][8];
 #pragma unroll
   for (int c = 0; c < CH; ++c)
@@ -179,9 +190,11 @@ skinny_kernel(Args p) {
   // chunks' loads below earlier chunks' MFMAs and serialize their latency.
   __builtin_amdgcn_sched_barrier(0);
 
+  // ---- activation slice -> LDS (waits only for the loads issued before B) ----
   if constexpr (kFused) {
     // 1 x block_k groups of G = block_k / 8 consecutive lanes (G divides 64
-    // and the slice width, so a group never straddles a wave or a row).
+    // and the slice width, so a group never straddles a wave or a row; the
+    // slice starts on a group boundary, so its group j is block kb0 + j).
     using Enc = typename std::conditional<fp8_fmt(KIND) == 1, e5m2_t, e4m3_t>::type;
     const int gl = p.block_k / 8;
 #pragma unroll
@@ -201,15 +214,29 @@ skinny_kernel(Args p) {
         if (pc % gl == 0) ss[row][pc / gl] = sc;
       }
     }
-    __syncthreads();
+  } else {
 #pragma unroll
-    for (int c = 0; c < CH; ++c) {
-      const int kl = min(kw + kChunk * c, k - kChunk) - kwg0;  // chunk start in the slice
+    for (int u = 0; u < kUA; ++u) {
+      const int piece = threadIdx.x + u * kThreads;
+      if (piece < kAPieces)
+        *reinterpret_cast<uint4*>(&sa[piece / (kSliceK / 16)][16 * (piece % (kSliceK / 16))]) = araw[u];
+    }
+    if constexpr (kBlock) {
 #pragma unroll
-      for (int f = 0; f < MB; ++f) {
-        av[c][f] = *reinterpret_cast<const uint2*>(&sa[4 * f + li / 4][kl + 8 * g]);
-        asc[c][f] = ss[4 * f + g][kl / p.block_k];
+      for (int u = 0; u < kUS; ++u) {
+        const int e = threadIdx.x + u * kThreads;
+        if (e < kRows * kSB) ss[e / kSB][e % kSB] = sraw[u];
       }
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int k0 = min(kw + kChunk * c, k - kChunk);  // chunk start (clamped past K)
+#pragma unroll
+    for (int f = 0; f < MB; ++f) {
+      av[c][f] = *reinterpret_cast<const uint2*>(&sa[4 * f + li / 4][k0 - kwg0 + 8 * g]);
+      if constexpr (kBlock) asc[c][f] = ss[4 * f + g][k0 / p.block_k - kb0];
     }
   }
 
