@@ -219,16 +219,17 @@ reduce_kernel(uint16_t* __restrict__ c, const float* __restrict__ ws,
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
   if (idx >= rows * n) return;
   const int64_t plane = rows * n;
-  float p[8];
   float o = 0.f;
-  int sp = 0;
-  for (; sp + 8 <= splits; sp += 8) {  // 8 independent loads in flight
+  // 8 independent loads in flight (clamped past the last split), added in
+  // split order; a runtime-count tail loop would serialize its loads.
+  for (int sp = 0; sp < splits; sp += 8) {
+    float p[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) p[i] = ws[(sp + i) * plane + idx];
+    for (int i = 0; i < 8; ++i) p[i] = ws[min(sp + i, splits - 1) * plane + idx];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) o += p[i];
+    for (int i = 0; i < 8; ++i)
+      if (sp + i < splits) o += p[i];
   }
-  for (; sp < splits; ++sp) o += ws[sp * plane + idx];
   if (bias) o += h2f<T>(bias[idx % n]);
   c[idx] = elem<T>::from_f32(o);
 }
@@ -465,8 +466,9 @@ void launch_gemv(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_
 
 // Split-plane reduce for the decode kernel: one workgroup per 256-column tile,
 // placed on the XCD whose workgroups wrote that tile's partials (workgroup ids
-// are dispatched to the 8 XCDs round-robin), so the planes are read from that
-// XCD's L2. Sums in split order, + bias.
+// are dispatched to the 8 XCDs round-robin by linear id, and with tiles % 8
+// == 0 a grid row keeps that mapping), so the planes are read from that XCD's
+// L2. Grid row y = output row. Sums in split order, + bias.
 template <typename T>
 __global__ void __launch_bounds__(w4dec::kTileN)
 dec_reduce_kernel(uint16_t* __restrict__ c, const float* __restrict__ ws,
@@ -477,20 +479,18 @@ dec_reduce_kernel(uint16_t* __restrict__ c, const float* __restrict__ ws,
   if (col >= n) return;
   const int64_t plane = static_cast<int64_t>(rows) * n;
   const float bv = bias ? h2f<T>(bias[col]) : 0.f;
-  for (int m = 0; m < rows; ++m) {
-    const float* p = ws + static_cast<int64_t>(m) * n + col;
+  const int m = blockIdx.y;  // one grid row per output row (no serial row loop)
+  const float* p = ws + static_cast<int64_t>(m) * n + col;
+  float o = 0.f;
+  for (int sp = 0; sp < splits; sp += 8) {  // 8 loads in flight, added in order
     float part[8];
-    float o = 0.f;
-    int sp = 0;
-    for (; sp + 8 <= splits; sp += 8) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) part[i] = p[(sp + i) * plane];
+    for (int i = 0; i < 8; ++i) part[i] = p[min(sp + i, splits - 1) * plane];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) o += part[i];
-    }
-    for (; sp < splits; ++sp) o += p[sp * plane];
-    c[static_cast<int64_t>(m) * n + col] = elem<T>::from_f32(o + bv);
+    for (int i = 0; i < 8; ++i)
+      if (sp + i < splits) o += part[i];
   }
+  c[static_cast<int64_t>(m) * n + col] = elem<T>::from_f32(o + bv);
 }
 
 template <typename T, int MB, int WAVES, int RPT, int ITER>
@@ -519,7 +519,7 @@ ks_status_t dec_rows(uint16_t* c, const uint16_t* a, const uint8_t* b, const uin
   launch_dec<T, MB, WAVES, RPT, ITER>(c, a, b, s, z, bias, mi, ni, ki, gs, tiles, splits,
                                       sc.partial, st);
   if (splits > 1)
-    hipLaunchKernelGGL((dec_reduce_kernel<T>), dim3(tiles), dim3(w4dec::kTileN), 0, st, c,
+    hipLaunchKernelGGL((dec_reduce_kernel<T>), dim3(tiles, static_cast<unsigned>(m)), dim3(w4dec::kTileN), 0, st, c,
                        sc.partial, bias, mi, ni, splits, tiles);
   return KS_SUCCESS;
 }
