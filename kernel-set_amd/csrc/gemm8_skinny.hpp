@@ -367,7 +367,15 @@ skinny_reduce_kernel(Args p) {
   if constexpr (KIND == INT8 || KIND == INT8_RAW) {
     const uint32_t* ws = static_cast<const uint32_t*>(p.ws) + idx;
     uint32_t s = 0;
-    for (int sp = 0; sp < p.splits; sp += 8) {  // 8 loads in flight, added in order
+    int sp = 0;
+    for (; sp + 8 <= p.splits; sp += 8) {  // 8 loads in flight, added in order
+      uint32_t part[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) part[i] = ws[(sp + i) * plane];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) s += part[i];
+    }
+    if (sp < p.splits) {  // tail: clamped, guarded, still one batch in flight
       uint32_t part[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) part[i] = ws[min(sp + i, p.splits - 1) * plane];
@@ -389,7 +397,15 @@ skinny_reduce_kernel(Args p) {
   } else {
     const float* ws = static_cast<const float*>(p.ws) + idx;
     float s = 0.f;
-    for (int sp = 0; sp < p.splits; sp += 8) {  // 8 loads in flight, added in order
+    int sp = 0;
+    for (; sp + 8 <= p.splits; sp += 8) {  // 8 loads in flight, added in order
+      float part[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) part[i] = ws[(sp + i) * plane];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) s += part[i];
+    }
+    if (sp < p.splits) {  // tail: clamped, guarded, still one batch in flight
       float part[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) part[i] = ws[min(sp + i, p.splits - 1) * plane];
