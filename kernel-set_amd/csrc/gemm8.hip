@@ -700,12 +700,13 @@ inline bool fast_ok(const Args& p) {
 
 template <int KIND, typename Out, bool UBS, bool SPLIT>
 void launch_fast_kernel(const Args& p, int64_t wgs, hipStream_t s) {
-  static bool configured = false;  // opt in to the LDS size once per process
-  if (!configured) {
+  // opt in to the LDS size once per process (thread-safe static initialization)
+  static const bool configured = [] {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm8_fast_kernel<KIND, Out, UBS, SPLIT>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kFastLds));
-    configured = true;
-  }
+    return true;
+  }();
+  (void)configured;
   hipLaunchKernelGGL((gemm8_fast_kernel<KIND, Out, UBS, SPLIT>), dim3(static_cast<unsigned>(wgs)),
                      dim3(kFThreads), kFastLds, s, p);
 }

@@ -529,13 +529,14 @@ ks_status_t ks_moe_compute_permutation(int32_t* sorted_token_ids, int32_t* exper
   if (num_experts > kMaxPermExperts)
     KS_FAIL(KS_ERROR_UNSUPPORTED_SHAPE, "ks_moe_compute_permutation: num_experts exceeds 2048");
   const size_t lds = (static_cast<size_t>(kPermWaves) * num_experts + kPermWaves + 1) * sizeof(int32_t);
-  static bool configured = false;
-  if (!configured) {
+  // opt in to the LDS size once per process (thread-safe static initialization)
+  static const bool configured = [] {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&permutation_kernel),
                               hipFuncAttributeMaxDynamicSharedMemorySize,
                               static_cast<int>((kPermWaves * kMaxPermExperts + kPermWaves + 1) * 4));
-    configured = true;
-  }
+    return true;
+  }();
+  (void)configured;
   auto s = to_stream(stream);
   hipLaunchKernelGGL(permutation_kernel, dim3(1), dim3(kPermThreads), lds, s, sorted_token_ids,
                      expert_offsets, topk_indices, static_cast<int32_t>(pairs), num_experts);

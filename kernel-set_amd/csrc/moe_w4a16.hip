@@ -112,12 +112,13 @@ void launch_pipe(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_
                  const uint16_t* z, const int32_t* offs, int E, int64_t rows, int64_t n,
                  int64_t k, int gs, hipStream_t st) {
   constexpr int lds = w4pipe::Ring<MB>::kBytes;
-  static bool configured = false;  // opt in to the LDS size once per process
-  if (!configured) {
+  // opt in to the LDS size once per process (thread-safe static initialization)
+  static const bool configured = [] {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_pipe_kernel<T, MB>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-    configured = true;
-  }
+    return true;
+  }();
+  (void)configured;
   const dim3 grid(static_cast<unsigned>((n + w4pipe::kTileN - 1) / w4pipe::kTileN),
                   static_cast<unsigned>(E));
   hipLaunchKernelGGL((moe_pipe_kernel<T, MB>), grid, dim3(w4pipe::kThreads), lds, st, c, a, b, s,

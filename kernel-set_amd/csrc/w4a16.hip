@@ -397,12 +397,13 @@ void launch_pipe(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_
                  const uint16_t* z, const uint16_t* bias, int64_t r0, int64_t r1, int64_t n,
                  int64_t k, int gs, int tiles, int splits, int sps, float* ws, hipStream_t st) {
   constexpr int lds = w4pipe::Ring<MB>::kBytes;
-  static bool configured = false;  // opt in to the LDS size once per process
-  if (!configured) {
+  // opt in to the LDS size once per process (thread-safe static initialization)
+  static const bool configured = [] {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&pipe_kernel<T, MB>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-    configured = true;
-  }
+    return true;
+  }();
+  (void)configured;
   hipLaunchKernelGGL((pipe_kernel<T, MB>), dim3(static_cast<unsigned>(tiles * splits)),
                      dim3(w4pipe::kThreads), lds, st, c, a, b, s, z, bias, r0, r1, n, k, gs,
                      splits, sps, ws);
@@ -450,12 +451,13 @@ void launch_dq(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_t*
                const uint16_t* z, const uint16_t* bias, int64_t m, int64_t n, int64_t k, int gs,
                hipStream_t st) {
   using C = w4dq::Cfg<BM, BN>;
-  static bool configured = false;  // opt in to the LDS size once per process
-  if (!configured) {
+  // opt in to the LDS size once per process (thread-safe static initialization)
+  static const bool configured = [] {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&w4dq::dq_kernel<T, BM, BN>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, C::kBytes);
-    configured = true;
-  }
+    return true;
+  }();
+  (void)configured;
   const dim3 grid(static_cast<unsigned>(n / BN), static_cast<unsigned>((m + BM - 1) / BM));
   hipLaunchKernelGGL((w4dq::dq_kernel<T, BM, BN>), grid, dim3(C::kThreads), C::kBytes, st, c, a, b,
                      s, z, bias, m, n, k, gs);
