@@ -770,6 +770,7 @@ inline bool skinny_ok(const Args& p) {
 
 template <int KIND, typename Out, int MB, int CH, typename In = void>
 ks_status_t launch_skinny(Args p, hipStream_t s, const char* who) {
+  constexpr bool kBlock = is_fp8_block(KIND);
   const int64_t tiles = (p.n + skinny::kTileN - 1) / skinny::kTileN;
   const int64_t kwg = static_cast<int64_t>(skinny::kWaves) * CH * skinny::kChunk;
   p.splits = static_cast<int>((p.k + kwg - 1) / kwg);
@@ -777,8 +778,13 @@ ks_status_t launch_skinny(Args p, hipStream_t s, const char* who) {
   ks_status_t st = get_scratch(s, static_cast<size_t>(p.splits) * p.m * p.n, 0, &sc, who);
   if (st != KS_SUCCESS) return st;
   p.ws = sc.partial;
-  hipLaunchKernelGGL((skinny::skinny_kernel<KIND, MB, CH, In>), dim3(static_cast<unsigned>(tiles * p.splits)),
-                     dim3(skinny::kThreads), 0, s, p);
+  const unsigned grid = static_cast<unsigned>(tiles * p.splits);
+  if (kBlock && p.block_k % (CH * skinny::kChunk) == 0)
+    hipLaunchKernelGGL((skinny::skinny_kernel<KIND, MB, CH, In, kBlock>), dim3(grid),
+                       dim3(skinny::kThreads), 0, s, p);
+  else
+    hipLaunchKernelGGL((skinny::skinny_kernel<KIND, MB, CH, In, false>), dim3(grid),
+                       dim3(skinny::kThreads), 0, s, p);
   hipLaunchKernelGGL((skinny::skinny_reduce_kernel<KIND, Out>),
                      dim3(static_cast<unsigned>((p.m * p.n + 255) / 256)), dim3(256), 0, s, p);
   return KS_SUCCESS;

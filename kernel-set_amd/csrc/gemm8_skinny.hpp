@@ -94,11 +94,19 @@ __device__ inline void act_to_f32(const uint4 w[2], float v[8]) {
 // whole groups) with the standalone quantizer's arithmetic (scale_from_amax,
 // enc8), then reads A codes and scales from LDS. Its activation loads are
 // issued before the B stream, so B stays in flight while it quantizes.
-template <int KIND, int MB, int CH, typename In = void>
+//
+// WB (blockwise only): block_k is a multiple of a wave's CH * 32 rows, so all
+// of a wave's chunks lie in one scale block; the MFMA then accumulates the
+// wave's whole K range and the partial is promoted once, O = P * (a_s * b_s)
+// (the same value as fma(P, a_s * b_s, 0)), which keeps the per-chunk O
+// registers out of the loop.
+template <int KIND, int MB, int CH, typename In = void, bool WB = false>
 __global__ void __launch_bounds__(kThreads)
 skinny_kernel(Args p) {
   constexpr bool kInt = KIND == INT8 || KIND == INT8_RAW;
   constexpr bool kBlock = is_fp8_block(KIND);
+  static_assert(!WB || kBlock, "one-block promotion serves the blockwise kinds");
+  constexpr bool kChunkPromote = kBlock && !WB;
   constexpr bool kFused = !std::is_void<In>::value;
   static_assert(!kFused || kBlock, "fused quantization serves the fp8 blockwise kinds");
   constexpr int kRows = 4 * MB;
@@ -281,7 +289,7 @@ skinny_kernel(Args p) {
           const uint4 v = bv[c][r];
           bq[r] = q == 0 ? v.x : q == 1 ? v.y : q == 2 ? v.z : v.w;
         }
-        const acc_t cin = kBlock ? acc_t{0, 0, 0, 0} : acc[f][q];
+        const acc_t cin = kChunkPromote ? acc_t{0, 0, 0, 0} : acc[f][q];
         if constexpr (kInt) {
           part[q] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
               i32x4{(int)fa[0], (int)fa[1], (int)fa[2], (int)fa[3]},
@@ -299,7 +307,7 @@ skinny_kernel(Args p) {
               cin, fmt, fmt, 0, 127, 0, 127);
         }
       }
-      if constexpr (kBlock) {
+      if constexpr (kChunkPromote) {
         const float sc = asc[c][f] * bsc[c];
 #pragma unroll
         for (int q = 0; q < 4; ++q)
@@ -309,6 +317,18 @@ skinny_kernel(Args p) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) acc[f][q] = part[q];
       }
+    }
+  }
+  if constexpr (WB) {
+    // Every chunk of the wave is in chunk 0's scale block (chunks past K
+    // added zeros).
+#pragma unroll
+    for (int f = 0; f < MB; ++f) {
+      const float sc = asc[0][f] * bsc[0];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[f][q][r] = fmaf(acc[f][q][r], sc, 0.f);
     }
   }
 
