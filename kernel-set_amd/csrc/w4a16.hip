@@ -447,7 +447,7 @@ ks_status_t run_pipe(uint16_t* c, const uint16_t* a, const uint8_t* b, const uin
 
 // Larger M: weights dequantized once per workgroup into LDS, 32x32x16 MFMA.
 template <typename T, int BM, int BN>
-void launch_dq(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_t* s,
+ks_status_t launch_dq(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_t* s,
                const uint16_t* z, const uint16_t* bias, int64_t m, int64_t n, int64_t k, int gs,
                hipStream_t st) {
   using C = w4dq::Cfg<BM, BN>;
@@ -458,9 +458,35 @@ void launch_dq(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_t*
     return true;
   }();
   (void)configured;
-  const dim3 grid(static_cast<unsigned>(n / BN), static_cast<unsigned>((m + BM - 1) / BM));
+  // Fewer than 192 workgroups: split K (whole quantization groups, at least two
+  // groups per split) and sum the partial plane with the split reduce. The
+  // kernel's stage loop is bound by the copy round trip of each stage, so a
+  // small grid otherwise runs its whole K serially on few CUs.
+  const int64_t wgs = (n / BN) * ((m + BM - 1) / BM);
+  const int nst = static_cast<int>(k / w4dq::kStageK);
+  const int spg = std::max(1, gs / w4dq::kStageK);
+  int splits = 1, sps = nst;
+  if (wgs < 192) {
+    splits = static_cast<int>(std::min<int64_t>((224 + wgs - 1) / wgs, nst / (2 * spg)));
+    if (splits > 1) {
+      sps = ((nst + splits - 1) / splits + spg - 1) / spg * spg;
+      splits = (nst + sps - 1) / sps;
+    } else {
+      splits = 1;
+      sps = nst;
+    }
+  }
+  Scratch sc;
+  if (splits > 1) {
+    ks_status_t r = get_scratch(st, static_cast<size_t>(splits) * m * n, 0, &sc, "ks_gemm_w4a16");
+    if (r != KS_SUCCESS) return r;
+  }
+  const dim3 grid(static_cast<unsigned>(n / BN), static_cast<unsigned>((m + BM - 1) / BM),
+                  static_cast<unsigned>(splits));
   hipLaunchKernelGGL((w4dq::dq_kernel<T, BM, BN>), grid, dim3(C::kThreads), C::kBytes, st, c, a, b,
-                     s, z, bias, m, n, k, gs);
+                     s, z, bias, m, n, k, gs, sps, splits > 1 ? sc.partial : nullptr);
+  if (splits > 1) launch_reduce<T>(c, sc.partial, bias, m, n, splits, st);
+  return KS_SUCCESS;
 }
 
 template <typename T, int RPT>
@@ -622,15 +648,17 @@ ks_status_t run(void* c_, const void* a_, const void* b_, const void* s_, const 
                   aligned(a, 16) && aligned(b, 16) && aligned(s, 4) && aligned(z, 4) &&
                   (m + 127) / 128 < 65536;
   if (dq) {
+    // Tile: the first of 128x128, 64x128, 128x64, 64x64 (wider N first: the
+    // activation re-reads, the dominant copy stream, scale with N / BN) that
+    // still gives >= 192 workgroups; the kernel is bound by each CU's copy
+    // stream, so an under-filled grid costs more than a smaller tile (M=256
+    // N=4096: 64 workgroups of 128x128 took 72.8 us).
     const bool wide = n % 128 == 0;
-    if (m > 64) {
-      if (wide) launch_dq<T, 128, 128>(c, a, b, s, z, bias, m, n, k, gs, st);
-      else launch_dq<T, 128, 64>(c, a, b, s, z, bias, m, n, k, gs, st);
-    } else {
-      if (wide) launch_dq<T, 64, 128>(c, a, b, s, z, bias, m, n, k, gs, st);
-      else launch_dq<T, 64, 64>(c, a, b, s, z, bias, m, n, k, gs, st);
-    }
-    return KS_SUCCESS;
+    auto wgs = [&](int bm, int bn) { return ((m + bm - 1) / bm) * ((n + bn - 1) / bn); };
+    if (m > 64 && wide && wgs(128, 128) >= 192) return launch_dq<T, 128, 128>(c, a, b, s, z, bias, m, n, k, gs, st);
+    if (wide && wgs(64, 128) >= 192) return launch_dq<T, 64, 128>(c, a, b, s, z, bias, m, n, k, gs, st);
+    if (m > 64 && wgs(128, 64) >= 192) return launch_dq<T, 128, 64>(c, a, b, s, z, bias, m, n, k, gs, st);
+    return launch_dq<T, 64, 64>(c, a, b, s, z, bias, m, n, k, gs, st);
   }
   if (pipe) return run_pipe<T>(c, a, b, s, z, bias, m, n, k, gs, st);
   if (mfma) return run_mfma<T>(c, a, b, s, z, bias, m, n, k, gs, st);

@@ -97,7 +97,7 @@ __global__ void __launch_bounds__((Cfg<BM, BN>::kThreads))
 dq_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
           const uint8_t* __restrict__ b, const uint16_t* __restrict__ scales,
           const uint16_t* __restrict__ zeros, const uint16_t* __restrict__ bias,
-          int64_t row_end, int64_t n, int64_t k, int gs) {
+          int64_t row_end, int64_t n, int64_t k, int gs, int sps, float* __restrict__ ws) {
   using R = Cfg<BM, BN>;
   constexpr int D = R::kDepth;
   constexpr int TM = BM / 64;  // 32x32 tiles per wave along M (wave tile BM/2 x 32)
@@ -109,7 +109,10 @@ dq_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * BN;
   const int64_t m0 = static_cast<int64_t>(blockIdx.y) * BM;
   const int t = threadIdx.x, lane = t % kWave, wave = t / kWave;
-  const int nst = static_cast<int>(k / kStageK);
+  // K split (grid z): stages [st0, st0 + nst); sps is a multiple of the
+  // stages per quantization group, so every split starts on a group.
+  const int st0 = static_cast<int>(blockIdx.z) * sps;
+  const int nst = min(static_cast<int>(k / kStageK) - st0, sps);
   auto wswz = [](int row) { return BN == 64 ? ((row >> 2) & 3) : (row & 7); };
 
   // ---- producer (direct global -> LDS), advanced one stage per issue() ----
@@ -119,7 +122,7 @@ dq_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
     const int row = 8 * (wave * R::kALoads + i) + lane / 8;
     const int cc = (lane % 8) ^ (row & 7);
     const int64_t gr = min<int64_t>(m0 + row, row_end - 1);
-    a_cur[i] = a + gr * k + 8 * cc;
+    a_cur[i] = a + gr * k + static_cast<int64_t>(st0) * kStageK + 8 * cc;
   }
   // W: the first half of the waves fill W, the second half a spare copy;
   // a 1 KB copy covers 1024 / BN packed rows.
@@ -127,15 +130,16 @@ dq_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
   const int wv = wave % (R::kWaves / 2);
   const int w_row = wv * kRowsPerCopy + lane / kWChunks;
   const int w_c = (lane % kWChunks) ^ wswz(w_row);
-  const uint8_t* w_cur = b + static_cast<int64_t>(w_row) * n + n0 + 16 * w_c;
+  const uint8_t* w_cur = b + (static_cast<int64_t>(st0) * (kStageK / 2) + w_row) * n + n0 + 16 * w_c;
   const int w_dst = (wave / (R::kWaves / 2)) * R::kWBytes + wv * 1024;
   // Scales / zeros of the stage's group, 2 columns per lane: BN = 64 -> lanes
   // 0-31 scales, 32-63 zeros of wave 0's copy; BN = 128 -> wave 0 scales,
   // wave 1 zeros. Scales stand in for absent zeros.
   const bool sz_zero_lane = BN == 64 ? lane >= 32 : (wave & 1) != 0;
   const int sz_c = BN == 64 ? 2 * (lane % 32) : 2 * lane;
-  const uint16_t* sz_col = ((sz_zero_lane && zeros) ? zeros : scales) + n0 + sz_c;
   const int spg = gs / kStageK;  // stages per quantization group
+  const uint16_t* sz_col = ((sz_zero_lane && zeros) ? zeros : scales) +
+                           static_cast<int64_t>(st0 / spg) * n + n0 + sz_c;
   int sz_left = spg;
   int is_slot = 0;
   auto issue = [&]() {
@@ -229,13 +233,17 @@ dq_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
 
   // ---- epilogue: acc[i][r] -> row 8*(r/4) + 4*lh + r%4 of the 32x32 tile ----
   const int64_t col = n0 + wc * 32 + l32;
-  const float bv = bias ? elem<T>::to_f32(bias[col]) : 0.f;
+  const float bv = (bias && !ws) ? elem<T>::to_f32(bias[col]) : 0.f;
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int64_t row = m0 + wr * (BM / 2) + i * 32 + 8 * (r / 4) + 4 * lh + (r % 4);
-      if (row < row_end) c[row * n + col] = elem<T>::from_f32(acc[i][r] + bv);
+      if (row >= row_end) continue;
+      if (ws)  // split partial, summed (with the bias) by the reduce kernel
+        ws[(static_cast<int64_t>(blockIdx.z) * row_end + row) * n + col] = acc[i][r];
+      else
+        c[row * n + col] = elem<T>::from_f32(acc[i][r] + bv);
     }
 }
 

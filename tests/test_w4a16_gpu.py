@@ -137,6 +137,15 @@ def test_batched_dtypes_bias_and_null_zeros(dt):
     check(70, 2048, 384, 128, zero_mode=None, dt=dt, bias=True, seed=7)
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_dq_split_k(dt):
+    # M > 64 on few column tiles: the dequantize-to-LDS GEMM splits K over
+    # whole groups and the split reduce adds the bias.
+    check(200, 4096, 512, 128, dt=dt, bias=True, seed=11)
+    check(65, 8192, 256, 64, zero_mode=None, dt=dt, seed=12)
+    check(130, 4096, 1024, 256, dt=dt, bias=True, seed=13)
+
+
 def test_batched_deterministic():
     a, codes, s, z = H.w4a16_inputs(64, 4096, 1024, 128, "int69", seed=8)
     b = O.pack_k2_uint8(codes)
