@@ -212,7 +212,6 @@ dq_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
     barrier_no_wait();  // Wd[st] visible, Wd[st+1] and ring slot st-1 free
     if (st + D - 1 < nst) issue();
     const int nx_slot = (slot_i + 1 == D) ? 0 : slot_i + 1;
-    if (st + 1 < nst) dequant(ring + nx_slot * R::kSlot + R::kABytes, wd + ((st + 1) & 1) * R::kWdBytes);
     const uint8_t* as = ring + slot_i * R::kSlot;
     const uint8_t* bs = wd + (st & 1) * R::kWdBytes;
 #pragma unroll
@@ -227,6 +226,9 @@ dq_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
         acc[i] = dq_traits<T>::mma(af, bf, acc[i]);
       }
     }
+    // The next stage's dequantization after this stage's MFMAs are issued:
+    // its VALU and LDS work then runs while the MFMAs execute.
+    if (st + 1 < nst) dequant(ring + nx_slot * R::kSlot + R::kABytes, wd + ((st + 1) & 1) * R::kWdBytes);
     slot_i = nx_slot;
   }
   wait_vmcnt<0>();
