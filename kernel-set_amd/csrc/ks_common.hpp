@@ -240,6 +240,23 @@ __device__ inline float scale_from_amax(float amax) {
 template <typename Enc>
 struct enc8;  // specialized per code type (int8 in quant.hip)
 
+// NaN codes are canonicalized to 0x7F (the code the reference's
+// __nv_fp8_e4m3 / __nv_fp8_e5m2 conversions give for the canonical NaN, and
+// the software encoders' code). The hardware converters keep a NaN's sign, and
+// the NaN this hardware produces for an invalid operation (an infinite group
+// amax gives inf * (1/inf) = inf * 0) has its sign bit set. Per byte b (SWAR):
+// e4m3 NaN iff (b & 0x7f) == 0x7f; e5m2 NaN iff (b & 0x7f) > 0x7c (no infinity
+// code can arise here: every other input is finite and |x * inv| <= qmax).
+__device__ inline uint32_t canon_nan_e4m3(uint32_t c) {
+  const uint32_t nan_sign = ((c & 0x7f7f7f7fu) + 0x01010101u) & 0x80808080u;
+  return c & ~nan_sign;  // 0xff -> 0x7f
+}
+__device__ inline uint32_t canon_nan_e5m2(uint32_t c) {
+  const uint32_t nan_hi = ((c & 0x7f7f7f7fu) + 0x03030303u) & 0x80808080u;
+  const uint32_t m = (nan_hi >> 7) * 0xffu;  // 0xff in each NaN byte
+  return (c & ~m) | (0x7f7f7f7fu & m);
+}
+
 template <>
 struct enc8<e4m3_t> {
   __device__ static inline uint2 run(const float v[8], float inv) {
@@ -247,7 +264,8 @@ struct enc8<e4m3_t> {
     lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[2] * inv, v[3] * inv, lo, true);
     int hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[4] * inv, v[5] * inv, 0, false);
     hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[6] * inv, v[7] * inv, hi, true);
-    return make_uint2(static_cast<uint32_t>(lo), static_cast<uint32_t>(hi));
+    return make_uint2(canon_nan_e4m3(static_cast<uint32_t>(lo)),
+                      canon_nan_e4m3(static_cast<uint32_t>(hi)));
   }
 };
 
@@ -258,7 +276,8 @@ struct enc8<e5m2_t> {
     lo = __builtin_amdgcn_cvt_pk_bf8_f32(v[2] * inv, v[3] * inv, lo, true);
     int hi = __builtin_amdgcn_cvt_pk_bf8_f32(v[4] * inv, v[5] * inv, 0, false);
     hi = __builtin_amdgcn_cvt_pk_bf8_f32(v[6] * inv, v[7] * inv, hi, true);
-    return make_uint2(static_cast<uint32_t>(lo), static_cast<uint32_t>(hi));
+    return make_uint2(canon_nan_e5m2(static_cast<uint32_t>(lo)),
+                      canon_nan_e5m2(static_cast<uint32_t>(hi)));
   }
 };
 

@@ -207,3 +207,65 @@ def test_dequantize_int4(dt):
     torch.cuda.synchronize()
     exp = O.round_to(O.dequant_int4(O.pack_k8_int32(codes), s, z, gs), dt)
     assert np.array_equal(H.from_dev_f32(out), exp)
+
+
+def _special_rows(cols):
+    """Rows with +-Inf, the largest finite floats, subnormals, exact rounding
+    ties and zeros (NaN is left out: the reference's `a > b ? a : b` amax
+    keeps or drops a NaN depending on its lane, so its result is not defined;
+    this build ignores NaN in amax, as the oracle does)."""
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((6, cols)).astype(np.float32)
+    x[0, 130] = np.inf
+    x[1, 3] = -np.inf
+    x[2, 0:4] = [3.0e38, -3.0e38, 1e-40, -1e-40]
+    x[3, :] = rng.uniform(-1, 1, cols).astype(np.float32) * np.float32(1e-39)
+    x[4, :8] = [448.0, -448.0, 464.0, 480.0, 0.5 * 2 ** -9, 1.5 * 2 ** -9, 57344.0, 61440.0]
+    x[5, :] = 0.0
+    return x
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("fmt", [O.E4M3, O.E5M2])
+@pytest.mark.parametrize("gs", [128, 64])
+def test_quantize_fp8_group_special_values(dt, fmt, gs):
+    cols = 512
+    t, xv = H.to_dev(_special_rows(cols), dt)
+    got_q, got_s = _group(t, 6, cols, gs, fmt, dt)
+    eq, es = O.quant_group(xv, gs, fmt)
+    assert np.array_equal(got_s.view(np.uint32), es.view(np.uint32))
+    assert np.array_equal(got_q, eq)
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("fmt", [O.E4M3, O.E5M2])
+@pytest.mark.parametrize("mode", [QuantMode.PER_TOKEN, QuantMode.PER_TENSOR])
+def test_quantize_fp8_rowwise_special_values(dt, fmt, mode):
+    cols = 512
+    x = _special_rows(cols)
+    if mode == QuantMode.PER_TENSOR:
+        x = x[2:]  # one infinity would make every code of the tensor NaN or 0
+    rows = x.shape[0]
+    t, xv = H.to_dev(x, dt)
+    fdt, tdt = FP8[fmt]
+    out = torch.empty(rows, cols, device=t.device, dtype=tdt)
+    sc = torch.empty(rows if mode == QuantMode.PER_TOKEN else 1, device=t.device, dtype=torch.float32)
+    ks.quant.quantize_fp8(out, sc, t, rows, cols, fp8_dtype=fdt, mode=mode)
+    torch.cuda.synchronize()
+    eq, es = (O.quant_row(xv, fmt) if mode == QuantMode.PER_TOKEN else O.quant_tensor(xv, fmt))
+    assert np.array_equal(sc.cpu().numpy().view(np.uint32), np.asarray(es, np.float32).view(np.uint32))
+    assert np.array_equal(H.u8(out), eq)
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_quantize_int8_special_values(dt):
+    cols = 512
+    x = _special_rows(cols)[2:]  # finite rows (int8 of an infinite scale is undefined)
+    t, xv = H.to_dev(x, dt)
+    out = torch.empty(4, cols, device=t.device, dtype=torch.int8)
+    sc = torch.empty(4, device=t.device, dtype=torch.float32)
+    ks.quant.quantize_int8(out, sc, t, 4, cols)
+    torch.cuda.synchronize()
+    eq, es = O.quant_row(xv, O.INT8)
+    assert np.array_equal(sc.cpu().numpy().view(np.uint32), es.view(np.uint32))
+    assert np.array_equal(H.u8(out), eq)
