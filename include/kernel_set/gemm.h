@@ -89,6 +89,29 @@ KS_API ks_status_t ks_gemm_fp8_blockwise_fused_quant(void* out, const void* a,
                                                      ks_dtype_t out_dtype,
                                                      ks_stream_t stream);
 
+/* Extension: no counterpart in the reference. For callers that hold bf16 /
+ * f16 / f32 activations and would otherwise call ks_quantize_int8 and then
+ * ks_gemm_w8a8 (the reference's dynamic int8 recipe, quant.h:42-46 +
+ * gemm.h:39-49). Defined as exactly that composition:
+ *   (a8, a_scale) = ks_quantize_int8(a, rows = m, cols = k, a_dtype, a_mode)
+ *   c             = ks_gemm_w8a8(a8, b_i8, a_scale, b_scale, bias, ..., a_mode, b_mode)
+ * and returns the same bits. a_mode is PER_TOKEN (one scale per row) or
+ * PER_TENSOR. For M <= 4 (N % 16 == 0, K % 32 == 0, 16-byte-aligned `a` and
+ * `b_i8`) it runs as one pass: every workgroup reduces the row maxima over the
+ * whole of K and quantizes its own K slice into LDS; otherwise it quantizes
+ * into library staging (per device and stream) and runs the GEMM.
+ * a_dtype f32/f16/bf16; out_dtype f32/f16/bf16; bias [N] in out_dtype or NULL. */
+KS_API ks_status_t ks_gemm_w8a8_fused_quant(void* c, const void* a,
+                                            const void* b_i8,
+                                            const float* b_scale,
+                                            const void* bias, int64_t m,
+                                            int64_t n, int64_t k,
+                                            ks_quant_mode_t a_mode,
+                                            ks_quant_mode_t b_mode,
+                                            ks_dtype_t a_dtype,
+                                            ks_dtype_t out_dtype,
+                                            ks_stream_t stream);
+
 KS_END_EXTERN_C
 
 #endif /* KERNEL_SET_GEMM_H_ */

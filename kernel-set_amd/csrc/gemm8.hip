@@ -1103,6 +1103,73 @@ ks_status_t ks_gemm_w8a8(void* c, const void* a_i8, const void* b_i8, const floa
   return KS_SUCCESS;
 }
 
+ks_status_t ks_gemm_w8a8_fused_quant(void* c, const void* a, const void* b_i8,
+                                     const float* b_scale, const void* bias, int64_t m, int64_t n,
+                                     int64_t k, ks_quant_mode_t a_mode, ks_quant_mode_t b_mode,
+                                     ks_dtype_t a_dtype, ks_dtype_t out_dtype,
+                                     ks_stream_t stream) {
+  static const char* who = "ks_gemm_w8a8_fused_quant";
+  KS_REQUIRE_PTR(c);
+  KS_REQUIRE_PTR(a);
+  KS_REQUIRE_PTR(b_i8);
+  KS_REQUIRE_PTR(b_scale);
+  if (m <= 0 || n <= 0 || k <= 0) KS_FAIL(KS_ERROR_INVALID_ARGUMENT, "ks_gemm_w8a8_fused_quant: bad shape");
+  if (a_mode != KS_QUANT_PER_TENSOR && a_mode != KS_QUANT_PER_TOKEN)
+    KS_FAIL(KS_ERROR_INVALID_ARGUMENT, "ks_gemm_w8a8_fused_quant: a_mode must be per-tensor or per-token");
+  if (b_mode != KS_QUANT_PER_TENSOR && b_mode != KS_QUANT_PER_CHANNEL)
+    KS_FAIL(KS_ERROR_INVALID_ARGUMENT, "ks_gemm_w8a8_fused_quant: b_mode must be per-tensor or per-channel");
+  if (a_dtype != KS_DTYPE_F32 && a_dtype != KS_DTYPE_F16 && a_dtype != KS_DTYPE_BF16)
+    KS_FAIL(KS_ERROR_UNSUPPORTED_DTYPE, "ks_gemm_w8a8_fused_quant: a_dtype must be f32/f16/bf16");
+  if (out_dtype != KS_DTYPE_F32 && out_dtype != KS_DTYPE_F16 && out_dtype != KS_DTYPE_BF16)
+    KS_FAIL(KS_ERROR_UNSUPPORTED_DTYPE, "ks_gemm_w8a8_fused_quant: out_dtype must be f32/f16/bf16");
+  if (mul_overflows(m, k) || mul_overflows(k, n) || mul_overflows(m, n) || m * n / kThreads >= kMaxTiles)
+    KS_FAIL(KS_ERROR_UNSUPPORTED_SHAPE, "ks_gemm_w8a8_fused_quant: shape exceeds grid limits");
+  if (k > 260000)  // 127*127*k must stay below 2^31 for exact int32 accumulation
+    KS_FAIL(KS_ERROR_UNSUPPORTED_SHAPE, "ks_gemm_w8a8_fused_quant: K too large for exact int32 accumulation");
+  auto s = to_stream(stream);
+  const bool per_token = a_mode == KS_QUANT_PER_TOKEN;
+  const size_t nscale = per_token ? static_cast<size_t>(m) : 1;
+  Args p{};
+  p.out = c;
+  p.a = static_cast<const uint8_t*>(a);  // the skinny checks see the activations as operand A
+  p.a_in = a;
+  p.b = static_cast<const uint8_t*>(b_i8);
+  p.b_scale = b_scale;
+  p.bias = bias;
+  p.m = m; p.n = n; p.k = k;
+  p.a_per_token = per_token;
+  p.b_per_channel = b_mode == KS_QUANT_PER_CHANNEL;
+  // One pass for M <= 4: every workgroup reduces the row maxima itself and
+  // quantizes its own K slice; workgroup 0 leaves the scales in library
+  // staging for the split reduce's epilogue. Measured on MI355X (graph replay,
+  // bf16 in/out, one pass vs quantize + GEMM): N = K = 4096 M = 1/4/8
+  // 9.9/10.9/13.6 us vs 10.8/11.8/13.1 us; N = K = 7168 15.8/16.4/21.5 us vs
+  // 16.5/17.6/19.5 us. Above M = 4 every workgroup's full-row pass costs more
+  // than the separate quantizer, so those shapes stage.
+  if (skinny_ok(p) && m <= 4) {
+    Scratch sc;
+    ks_status_t st = get_scratch(s, 0, nscale * sizeof(float), &sc, who);
+    if (st != KS_SUCCESS) return st;
+    p.a_scale_out = static_cast<float*>(sc.staging);
+    p.a_scale = p.a_scale_out;
+    st = run_fused<INT8>(p, a_dtype, out_dtype, s, who);
+    if (st != KS_SUCCESS) return st;
+    KS_LAUNCH_STATUS("ks_gemm_w8a8_fused_quant");
+    return KS_SUCCESS;
+  }
+  // Otherwise the int8 quantizer writes codes and scales to library staging
+  // and the W8A8 GEMM reads them (same stream, so ordered).
+  const size_t codes = static_cast<size_t>((m * k + 255) / 256 * 256);
+  Scratch sc;
+  ks_status_t st = get_scratch(s, 0, codes + nscale * sizeof(float), &sc, who);
+  if (st != KS_SUCCESS) return st;
+  uint8_t* a8 = static_cast<uint8_t*>(sc.staging);
+  float* a_s = reinterpret_cast<float*>(a8 + codes);
+  st = ks_quantize_int8(a8, a_s, a, m, k, a_dtype, a_mode, stream);
+  if (st != KS_SUCCESS) return st;
+  return ks_gemm_w8a8(c, a8, b_i8, a_s, b_scale, bias, m, n, k, a_mode, b_mode, out_dtype, stream);
+}
+
 ks_status_t ks_testing_gemm_w8a8_i32(int32_t* acc, const void* a_i8, const void* b_i8,
                                      int64_t m, int64_t n, int64_t k, ks_stream_t stream) {
   KS_REQUIRE_PTR(acc);

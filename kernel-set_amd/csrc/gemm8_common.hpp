@@ -40,6 +40,7 @@ struct Args {
   int splits;                      // skinny path: K splits
   void* ws;                        // skinny path: split partial plane
   const void* a_in;                // fused quantize + GEMM: unquantized activations [M, K]
+  float* a_scale_out;              // fused int8: workgroup 0 publishes the activation scales
 };
 
 }  // namespace gemm8

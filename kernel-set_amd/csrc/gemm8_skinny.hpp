@@ -88,12 +88,20 @@ __device__ inline void act_to_f32(const uint4 w[2], float v[8]) {
 // a and b 16-byte aligned, M*K, K*N and splits*M*N below 2^31;
 // blockwise: block_k % 32 == 0, block_n % 16 == 0.
 //
-// In != void: fused activation quantization (fp8 blockwise kinds only). The
-// workgroup quantizes its own slice A_in[0:M, kwg0 : kwg0 + 256*CH] into LDS
-// in 1 x block_k groups (block_k in {32, 64, 128, 256}, so the slice holds
-// whole groups) with the standalone quantizer's arithmetic (scale_from_amax,
-// enc8), then reads A codes and scales from LDS. Its activation loads are
-// issued before the B stream, so B stays in flight while it quantizes.
+// In != void: fused activation quantization. The workgroup quantizes its own
+// slice A_in[0:M, kwg0 : kwg0 + 256*CH] into LDS with the standalone
+// quantizer's arithmetic (scale_from_amax, enc8), then reads A codes (and
+// scales) from LDS. Its slice loads are issued before the B stream, so B stays
+// in flight while it quantizes.
+//  * fp8 blockwise kinds: 1 x block_k groups (block_k in {32, 64, 128, 256},
+//    so the slice holds whole groups).
+//  * INT8: per-token (a_per_token) or per-tensor scales, which need the amax
+//    of whole rows. A prologue, run before any other load while the registers
+//    are free, reads all M x K activations (they stay in L2: every workgroup
+//    reads the same M <= 8 rows) and reduces the row maxima (fmaxf, so the
+//    order does not change the value). Every workgroup derives the same
+//    scales; workgroup 0 also writes them to a_scale_out, from which the split
+//    reduce takes the epilogue's a_s.
 //
 // WB (blockwise only): block_k is a multiple of a wave's CH * 32 rows, so all
 // of a wave's chunks lie in one scale block; the MFMA then accumulates the
@@ -108,7 +116,8 @@ skinny_kernel(Args p) {
   static_assert(!WB || kBlock, "one-block promotion serves the blockwise kinds");
   constexpr bool kChunkPromote = kBlock && !WB;
   constexpr bool kFused = !std::is_void<In>::value;
-  static_assert(!kFused || kBlock, "fused quantization serves the fp8 blockwise kinds");
+  static_assert(!kFused || kBlock || KIND == INT8, "fused quantization: fp8 blockwise or INT8");
+  constexpr bool kFusedI8 = kFused && KIND == INT8;
   constexpr int kRows = 4 * MB;
   constexpr int kSliceK = kWaves * CH * kChunk;  // k-rows per workgroup
   __shared__ uint32_t red[kWaves / 2][kRows][kTileN];
@@ -131,6 +140,60 @@ skinny_kernel(Args p) {
   const int kwg0 = split * kSliceK;
   const int kw = kwg0 + wave * CH * kChunk;
   const int kb0 = kBlock ? kwg0 / p.block_k : 0;  // first scale block of the slice
+
+  __shared__ float srow[kRows];
+  // ---- fused int8: per-row (or per-tensor) scales from a full-row prologue.
+  // (Issuing its loads behind the B stream instead measured no faster: the
+  // first MFMA then waits for the whole stream.)
+  if constexpr (kFusedI8) {
+    using S = typename In::storage;
+    const S* x = static_cast<const S*>(p.a_in);
+    const int ppr = k / 8;  // 8-element pieces per row (K % 32 == 0)
+    const int np = m * ppr;
+    float ra[kRows];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) ra[r] = 0.f;
+    for (int base = 0; base < np; base += 8 * kThreads) {
+      uint4 w[8][2];  // 8 pieces in flight; rows are contiguous, so piece i is x + 8i
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        load8_act_raw<In>(x + 8 * static_cast<int64_t>(min(base + i * kThreads + static_cast<int>(threadIdx.x), np - 1)), w[i]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int pc = base + i * kThreads + static_cast<int>(threadIdx.x);
+        float v[8];
+        act_to_f32<In>(w[i], v);
+        float am = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) am = fmaxf(am, fabsf(v[e]));
+        const int row = pc < np ? pc / ppr : kRows;  // kRows: dropped
+#pragma unroll
+        for (int r = 0; r < kRows; ++r) ra[r] = row == r ? fmaxf(ra[r], am) : ra[r];
+      }
+    }
+    __shared__ float rmax[kWaves][kRows];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+      const float v = wave_max(ra[r]);
+      if (lane == 0) rmax[wave][r] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x < kRows) {
+      float am = 0.f;
+      if (p.a_per_token) {
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) am = fmaxf(am, rmax[w][threadIdx.x]);
+      } else {
+        for (int r = 0; r < m; ++r)
+#pragma unroll
+          for (int w = 0; w < kWaves; ++w) am = fmaxf(am, rmax[w][r]);
+      }
+      const float sc = scale_from_amax<i8_t>(am);
+      srow[threadIdx.x] = sc;
+      if (blockIdx.x == 0 && static_cast<int>(threadIdx.x) < (p.a_per_token ? m : 1))
+        p.a_scale_out[threadIdx.x] = sc;
+    }
+  }
 
   // ---- loads, in issue order: activation slice, scales, then B ----
   // Fused: unquantized activations, 8 elements per slot.
@@ -197,9 +260,21 @@ skinny_kernel(Args p) {
   // Keep every load above the math: the scheduler would otherwise sink later
   // chunks' loads below earlier chunks' MFMAs and serialize their latency.
   __builtin_amdgcn_sched_barrier(0);
-
   // ---- activation slice -> LDS (waits only for the loads issued before B) ----
-  if constexpr (kFused) {
+  if constexpr (kFusedI8) {
+    __syncthreads();  // srow complete
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int slot = threadIdx.x + u * kThreads;
+      const int row = slot / kPieces, pc = slot % kPieces;
+      float xv[8];
+      act_to_f32<In>(xr[u], xv);
+      // Rows past M and pieces past K hold clamped loads; the math masks them.
+      const float inv = 1.0f / srow[row < kRows ? row : 0];
+      const uint2 code = enc8<i8_t>::run(xv, inv);
+      if (slot < kSlots) *reinterpret_cast<uint2*>(&sa[row][8 * pc]) = code;
+    }
+  } else if constexpr (kFused) {
     // 1 x block_k groups of G = block_k / 8 consecutive lanes (G divides 64
     // and the slice width, so a group never straddles a wave or a row; the
     // slice starts on a group boundary, so its group j is block kb0 + j).

@@ -238,7 +238,7 @@ __device__ inline float scale_from_amax(float amax) {
 // they see is x * (1/s) with s >= amax/qmax, so |x/s| <= qmax(1 + 2^-23) and
 // the saturating and non-saturating conversions give the same code.
 template <typename Enc>
-struct enc8;  // specialized per code type (int8 in quant.hip)
+struct enc8;  // specialized per code type
 
 // NaN codes are canonicalized to 0x7F (the code the reference's
 // __nv_fp8_e4m3 / __nv_fp8_e5m2 conversions give for the canonical NaN, and
@@ -281,6 +281,30 @@ struct enc8<e5m2_t> {
   }
 };
 
+
+// int8 code: round-half-even of the scaled value clamped to [-127, 127]
+// (quant_int8.cu:44 and :80 of cklxx/kernel-set).
+struct i8_t {
+  static constexpr float qmax = kInt8Max;
+  __device__ static inline uint8_t enc(float v) {
+    // Same comparison order as a clamp written v<lo?lo:(v>hi?hi:v).
+    const float c = v < -kInt8Max ? -kInt8Max : (v > kInt8Max ? kInt8Max : v);
+    return static_cast<uint8_t>(static_cast<int8_t>(static_cast<int>(__builtin_rintf(c))));
+  }
+};
+
+template <>
+struct enc8<i8_t> {
+  __device__ static inline uint2 run(const float v[8], float inv) {
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      lo |= static_cast<uint32_t>(i8_t::enc(v[i] * inv)) << (8 * i);
+      hi |= static_cast<uint32_t>(i8_t::enc(v[i + 4] * inv)) << (8 * i);
+    }
+    return make_uint2(lo, hi);
+  }
+};
 
 // ---------------------------------------------------------------------------
 // wave64 reductions (xor butterflies over all 64 lanes)

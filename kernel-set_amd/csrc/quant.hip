@@ -59,14 +59,7 @@ __device__ inline void load8<f32_t>(const float* p, float v[8]) {
 }
 
 // ---- encoders: scaled fp32 value -> one code byte -------------------------
-struct i8_t {
-  static constexpr float qmax = kInt8Max;
-  __device__ static inline uint8_t enc(float v) {
-    // Same comparison order as a clamp written v<lo?lo:(v>hi?hi:v).
-    const float c = v < -kInt8Max ? -kInt8Max : (v > kInt8Max ? kInt8Max : v);
-    return static_cast<uint8_t>(static_cast<int8_t>(static_cast<int>(__builtin_rintf(c))));
-  }
-};
+// i8_t (the int8 encoder) and its enc8 live in ks_common.hpp.
 
 
 template <typename Enc>
@@ -96,18 +89,7 @@ __device__ inline void store8(uint8_t* dst, const float v[8], float inv) {
 // enc8<e4m3_t> / enc8<e5m2_t> (hardware converters) live in ks_common.hpp.
 }  // namespace quant
 
-template <>
-struct enc8<quant::i8_t> {
-  __device__ static inline uint2 run(const float v[8], float inv) {
-    uint32_t lo = 0, hi = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      lo |= static_cast<uint32_t>(quant::i8_t::enc(v[i] * inv)) << (8 * i);
-      hi |= static_cast<uint32_t>(quant::i8_t::enc(v[i + 4] * inv)) << (8 * i);
-    }
-    return make_uint2(lo, hi);
-  }
-};
+
 
 namespace quant {
 

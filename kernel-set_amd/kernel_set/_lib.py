@@ -152,6 +152,8 @@ _decl("ks_gemm_fp8_blockwise",
 # extension of this build (no reference counterpart)
 _decl("ks_gemm_fp8_blockwise_fused_quant",
       [_VP, _VP, _VP, _F32P, _I64, _I64, _I64, _I, _I, _I, _I, _I, _VP])
+_decl("ks_gemm_w8a8_fused_quant",
+      [_VP, _VP, _VP, _F32P, _VP, _I64, _I64, _I64, _I, _I, _I, _I, _VP])
 # quant.h
 _decl("ks_quantize_fp8", [_VP, _F32P, _VP, _I64, _I64, _I, _I, _I, _VP])
 _decl("ks_dequantize_fp8", [_VP, _VP, _F32P, _I64, _I64, _I, _I, _I, _VP])

@@ -45,6 +45,26 @@ def gemm_w8a8(c: TensorLike, a_i8: TensorLike, b_i8: TensorLike, a_scale: Tensor
     return c
 
 
+def gemm_w8a8_fused_quant(c: TensorLike, a: TensorLike, b_i8: TensorLike,
+                          b_scale: TensorLike, m: int, n: int, k: int,
+                          bias: TensorLike = None, a_mode: int = QuantMode.PER_TOKEN,
+                          b_mode: int = QuantMode.PER_CHANNEL, a_dtype: int = None,
+                          out_dtype: int = None, stream: TensorLike = None) -> TensorLike:
+    """Extension (no reference counterpart): ``c = gemm_w8a8(quantize_int8(a,
+    a_mode), b_i8, b_scale, bias)`` with the same bits as that two-call
+    sequence. ``a`` is bf16/f16/f32 ``[M, K]``; decode shapes (M <= 4) run as
+    a single pass."""
+    adt = infer_dtype(a, a_dtype)
+    odt = _out_dtype(c, out_dtype, "ks_gemm_w8a8_fused_quant")
+    check(lib.ks_gemm_w8a8_fused_quant(
+        ptr(c, name="c"), ptr(a, name="a"), ptr(b_i8, name="b_i8"),
+        _f32(b_scale, name="b_scale"), ptr(bias, name="bias"), int(m), int(n), int(k),
+        int(a_mode), int(b_mode), adt, odt,
+        default_stream(stream, c if not isinstance(c, int) else a)),
+        "ks_gemm_w8a8_fused_quant")
+    return c
+
+
 def gemm_w4a16(c: TensorLike, a: TensorLike, b_packed: TensorLike, scales: TensorLike,
                zeros: TensorLike, m: int, n: int, k: int, group_size: int,
                bias: TensorLike = None, dtype: Optional[int] = None,

@@ -143,6 +143,28 @@ def test_fp8_blockwise_fused_quant_validation():
     assert f(P, P, P, fp, big, big, 8, 128, 128, *ok) == Status.ERROR_UNSUPPORTED_SHAPE
 
 
+def test_w8a8_fused_quant_validation():
+    # extension entry point: pointers, shape, modes, dtypes, then the K limit
+    f = _lib.lib.ks_gemm_w8a8_fused_quant
+    fp = ctypes.cast(P, _lib._F32P)
+    modes = (QuantMode.PER_TOKEN, QuantMode.PER_CHANNEL)
+    ok = (DType.BF16, DType.BF16, None)
+    assert f(P, P, P, None, None, 1, 1, 1, *modes, *ok) == Status.ERROR_INVALID_ARGUMENT
+    assert ks.last_error_string() == "null arg: b_scale"
+    assert f(P, P, P, fp, None, 1, 0, 1, *modes, *ok) == Status.ERROR_INVALID_ARGUMENT
+    assert f(P, P, P, fp, None, 1, 1, 1, QuantMode.PER_CHANNEL, QuantMode.PER_CHANNEL, *ok) \
+        == Status.ERROR_INVALID_ARGUMENT
+    assert f(P, P, P, fp, None, 1, 1, 1, QuantMode.PER_TOKEN, QuantMode.PER_TOKEN, *ok) \
+        == Status.ERROR_INVALID_ARGUMENT
+    assert f(P, P, P, fp, None, 1, 1, 1, *modes, DType.I8, DType.BF16, None) \
+        == Status.ERROR_UNSUPPORTED_DTYPE
+    assert f(P, P, P, fp, None, 1, 1, 1, *modes, DType.BF16, DType.I8, None) \
+        == Status.ERROR_UNSUPPORTED_DTYPE
+    assert f(P, P, P, fp, None, 1, 16, 300000, *modes, *ok) == Status.ERROR_UNSUPPORTED_SHAPE
+    big = 1 << 40
+    assert f(P, P, P, fp, None, big, big, 8, *modes, *ok) == Status.ERROR_UNSUPPORTED_SHAPE
+
+
 def test_fp8_blockwise_validation():
     f = _lib.lib.ks_gemm_fp8_blockwise
     fp = ctypes.cast(P, _lib._F32P)

@@ -67,6 +67,14 @@ def _w8a8(m, n, k, g):
                                      b_mode=QuantMode.PER_CHANNEL), c
 
 
+def _w8a8_fused(m, n, k, g, a_mode=QuantMode.PER_TOKEN):
+    x = torch.randn(m, k, device=DEV, generator=g).to(torch.bfloat16)
+    b = torch.randint(-127, 128, (k, n), device=DEV, dtype=torch.int8, generator=g)
+    b_s = torch.rand(n, device=DEV, generator=g) * 0.02 + 0.01
+    c = torch.empty(m, n, device=DEV, dtype=torch.bfloat16)
+    return lambda: ks.gemm.gemm_w8a8_fused_quant(c, x, b, b_s, m, n, k, a_mode=a_mode), c
+
+
 def _quant_group(m, k, g):
     x = torch.randn(m, k, device=DEV, generator=g).to(torch.bfloat16)
     q = torch.empty(m, k, device=DEV, dtype=torch.float8_e4m3fn)
@@ -90,6 +98,9 @@ CASES = {
     "fp8_plain_skinny_M3": lambda g: _fp8_plain(3, 4096, 2048, g),
     "w8a8_skinny_M2": lambda g: _w8a8(2, 4096, 4096, g),
     "w8a8_splitk_M128": lambda g: _w8a8(128, 1024, 4096, g),
+    "w8a8_fused_M3": lambda g: _w8a8_fused(3, 2048, 4096, g),
+    "w8a8_fused_tensor_M2": lambda g: _w8a8_fused(2, 2048, 2048, g, QuantMode.PER_TENSOR),
+    "w8a8_fused_staged_M24": lambda g: _w8a8_fused(24, 2048, 2048, g),
     "quant_group_2048x7168": lambda g: _quant_group(2048, 7168, g),
 }
 
