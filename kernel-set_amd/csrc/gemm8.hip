@@ -292,7 +292,13 @@ gemm8_kernel(Args p) {
 //    The copies for step s+1 are issued as inline asm before step s's math,
 //    so they overlap it (the compiler would otherwise hold every LDS read of
 //    step s behind them with a vmcnt(0)).
-//  * A fragments: two ds_read_b128 per 16x(32 k) lane slice.
+//  * A fragments: two ds_read_b128 per 16x(32 k) lane slice. The 32 bytes of
+//    lane group lk (lane / 16) are k = 16lk..16lk+15 and 64+16lk..64+16lk+15
+//    of the 128-k step, and the B fragments read the same k-rows in the same
+//    byte order (any k order shared by A and B gives the same dot products).
+//    With k = 32lk..32lk+31 instead, every A read was a 2-way bank conflict
+//    (SQ_LDS_BANK_CONFLICT a third of the LDS active cycles); this order is
+//    the W8A8 path's and reads conflict-free.
 //  * B fragments are read already transposed with ds_read_b64_tr_b8: in each
 //    16-lane group, lanes (2j, 2j+1) address the two 8-byte halves of k-row j
 //    of a 16-column block and lane i receives column i of those 8 rows, i.e.
@@ -451,7 +457,7 @@ gemm8_fast_kernel(Args p) {
       // sched_barrier pins this order against the scheduler's reordering.
       // A fragment: the chunk swizzle of row wm + 16i + li is a_swz(li) for every i.
       const uint8_t* pa0 = a_src + (wm + li) * kFARow;
-      const int ca0 = ((2 * lk) ^ a_swz(li)) * 16, ca1 = ((2 * lk + 1) ^ a_swz(li)) * 16;
+      const int ca0 = (lk ^ a_swz(li)) * 16, ca1 = ((4 + lk) ^ a_swz(li)) * 16;
       const float* sa0 = &sAs[cur * kFBM + wm + 4 * lk];
       uint4 xa[8][2];
       f32x4 scl[8];
@@ -465,8 +471,8 @@ gemm8_fast_kernel(Args p) {
       float bs[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const i32x2 q0 = b_tr8(j, 32 * lk + 0), q1 = b_tr8(j, 32 * lk + 8);
-        const i32x2 q2 = b_tr8(j, 32 * lk + 16), q3 = b_tr8(j, 32 * lk + 24);
+        const i32x2 q0 = b_tr8(j, 16 * lk + 0), q1 = b_tr8(j, 16 * lk + 8);
+        const i32x2 q2 = b_tr8(j, 64 + 16 * lk), q3 = b_tr8(j, 64 + 16 * lk + 8);
         fb[j] = i32x8{q0[0], q0[1], q1[0], q1[1], q2[0], q2[1], q3[0], q3[1]};
         bs[j] = sBs[cur * kFBN + wn + 16 * j + li];
       }
@@ -506,14 +512,14 @@ gemm8_fast_kernel(Args p) {
       // A fragments are read one row block ahead of their MFMAs.
       constexpr int fmt = fp8_fmt(KIND);
       const uint8_t* pa0 = a_src + (wm + li) * kFARow;
-      const int ca0 = ((2 * lk) ^ a_swz(li)) * 16, ca1 = ((2 * lk + 1) ^ a_swz(li)) * 16;
+      const int ca0 = (lk ^ a_swz(li)) * 16, ca1 = ((4 + lk) ^ a_swz(li)) * 16;
       uint4 xa0 = *reinterpret_cast<const uint4*>(pa0 + ca0);
       uint4 xa1 = *reinterpret_cast<const uint4*>(pa0 + ca1);
       i32x8 fbp[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const i32x2 q0 = b_tr8(j, 32 * lk + 0), q1 = b_tr8(j, 32 * lk + 8);
-        const i32x2 q2 = b_tr8(j, 32 * lk + 16), q3 = b_tr8(j, 32 * lk + 24);
+        const i32x2 q0 = b_tr8(j, 16 * lk + 0), q1 = b_tr8(j, 16 * lk + 8);
+        const i32x2 q2 = b_tr8(j, 64 + 16 * lk), q3 = b_tr8(j, 64 + 16 * lk + 8);
         fbp[j] = i32x8{q0[0], q0[1], q1[0], q1[1], q2[0], q2[1], q3[0], q3[1]};
       }
 #pragma unroll
