@@ -34,6 +34,7 @@
 #include "w4a16_mfma.hpp"
 #include "w4a16_pipe.hpp"
 #include "w4a16_dq.hpp"
+#include "w4a16_dqs.hpp"
 #include "w4a16_dec.hpp"
 #include "workspace.hpp"
 
@@ -451,10 +452,18 @@ ks_status_t launch_dq(uint16_t* c, const uint16_t* a, const uint8_t* b, const ui
                const uint16_t* z, const uint16_t* bias, int64_t m, int64_t n, int64_t k, int gs,
                hipStream_t st) {
   using C = w4dq::Cfg<BM, BN>;
+  // 128 x 128 tiles run the role-split kernel (w4a16_dqs.hpp), the others dq_kernel.
+  constexpr bool kSplitRoles = BM == 128 && BN == 128;
+  constexpr int kLds = kSplitRoles ? w4dqs::kBytes : C::kBytes;
+  constexpr unsigned kBlock = kSplitRoles ? w4dqs::kThreads : C::kThreads;
   // opt in to the LDS size once per process (thread-safe static initialization)
   static const bool configured = [] {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&w4dq::dq_kernel<T, BM, BN>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, C::kBytes);
+    if constexpr (kSplitRoles)
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&w4dqs::dqs_kernel<T>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
+    else
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&w4dq::dq_kernel<T, BM, BN>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
     return true;
   }();
   (void)configured;
@@ -483,8 +492,12 @@ ks_status_t launch_dq(uint16_t* c, const uint16_t* a, const uint8_t* b, const ui
   }
   const dim3 grid(static_cast<unsigned>(n / BN), static_cast<unsigned>((m + BM - 1) / BM),
                   static_cast<unsigned>(splits));
-  hipLaunchKernelGGL((w4dq::dq_kernel<T, BM, BN>), grid, dim3(C::kThreads), C::kBytes, st, c, a, b,
-                     s, z, bias, m, n, k, gs, sps, splits > 1 ? sc.partial : nullptr);
+  if constexpr (kSplitRoles)
+    hipLaunchKernelGGL((w4dqs::dqs_kernel<T>), grid, dim3(kBlock), kLds, st, c, a, b, s, z, bias, m,
+                       n, k, gs, sps, splits > 1 ? sc.partial : nullptr);
+  else
+    hipLaunchKernelGGL((w4dq::dq_kernel<T, BM, BN>), grid, dim3(kBlock), kLds, st, c, a, b, s, z,
+                       bias, m, n, k, gs, sps, splits > 1 ? sc.partial : nullptr);
   if (splits > 1) launch_reduce<T>(c, sc.partial, bias, m, n, splits, st);
   return KS_SUCCESS;
 }

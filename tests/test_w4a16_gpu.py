@@ -146,6 +146,19 @@ def test_dq_split_k(dt):
     check(130, 4096, 1024, 256, dt=dt, bias=True, seed=13)
 
 
+@pytest.mark.parametrize("m,k,n,gs,zero_mode,dt,bias", [
+    (129, 1024, 12288, 128, "int69", "bf16", False),
+    (200, 2048, 12288, 64, None, "f16", True),
+    (256, 1024, 12288, 256, "int69", "bf16", True),
+    (300, 512, 16384, 128, "int69", "f16", False),
+])
+def test_dq_role_split_tiles(m, k, n, gs, zero_mode, dt, bias):
+    # M > 64 with >= 192 tiles of 128 x 128: the role-split kernel (producer
+    # waves copy and dequantize, consumer waves run the MFMAs); M not a
+    # multiple of 128 leaves a ragged last row tile.
+    check(m, k, n, gs, zero_mode=zero_mode, dt=dt, seed=m + gs, bias=bias)
+
+
 def test_batched_deterministic():
     a, codes, s, z = H.w4a16_inputs(64, 4096, 1024, 128, "int69", seed=8)
     b = O.pack_k2_uint8(codes)
