@@ -325,21 +325,36 @@ __device__ inline int a_swz(int row) { return (row >> 1) & 7; }
 __device__ inline int b_swz(int row) { return (row & 7) | ((((row >> 4) ^ (row >> 5)) & 1) << 3); }
 typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
 
+// LDS buffers of the fast kernel per tile height (see gemm8_fast_kernel).
+constexpr int fast_nb(int bm) { return bm == 64 ? 3 : 2; }
+
+// s_waitcnt vmcnt(N) only (expcnt and lgkmcnt left at their maxima).
+template <int N>
+__device__ inline void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 // SPLIT: workgroup id = tile * p.splits + split; the split runs K steps
 // [split * per, min(steps, (split + 1) * per)) and writes its raw accumulators
 // (fp8 blockwise: the promoted O; plain fp8: the fp32 sum; int8: int32) to the
 // partial plane p.ws, which skinny::skinny_reduce_kernel sums in split order
 // before the epilogue.
-template <int KIND, typename Out, bool UNIFORM_BS, bool SPLIT>
+template <int KIND, typename Out, bool UNIFORM_BS, bool SPLIT, int BM>
 __global__ void __launch_bounds__(kFThreads)
 gemm8_fast_kernel(Args p) {
+  // BM = 256 or 64 rows per tile: each wave owns BM/2 rows = kRB 16-row
+  // blocks and issues kAL of the tile's 1 KB A copies per K step. NB LDS
+  // buffers: 64-row tiles leave room for three, so two steps of copies are in
+  // flight (their splits run few steps, each bound by the copy round trip).
+  constexpr int kRB = BM / 32, kAL = BM / 64, NB = fast_nb(BM);
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  uint8_t* sA = smem;                                   // [2][256][128]
-  uint8_t* sB = smem + 2 * kFBM * kFARow;               // [2][128][256]
-  float* sAs = reinterpret_cast<float*>(sB + 2 * kBK * kFBRow);  // [2][256]
-  float* sBs = sAs + 2 * kFBM;                                   // [2][256]
+  uint8_t* sA = smem;                                    // [NB][BM][128]
+  uint8_t* sB = smem + NB * BM * kFARow;                 // [NB][128][256]
+  float* sAs = reinterpret_cast<float*>(sB + NB * kBK * kFBRow);  // [NB][256]
+  float* sBs = sAs + NB * kFBM;                                    // [NB][256]
 
-  const int tiles_m = static_cast<int>((p.m + kFBM - 1) / kFBM);
+  const int tiles_m = static_cast<int>((p.m + BM - 1) / BM);
   const int tiles_n = static_cast<int>(p.n / kFBN);
   int tm, tn;
   int bid = blockIdx.x, split = 0;
@@ -348,26 +363,30 @@ gemm8_fast_kernel(Args p) {
     bid /= p.splits;
   }
   tile_coords(bid, tiles_m, tiles_n, &tm, &tn);
-  const int64_t m0 = static_cast<int64_t>(tm) * kFBM;
+  const int64_t m0 = static_cast<int64_t>(tm) * BM;
   const int64_t n0 = static_cast<int64_t>(tn) * kFBN;
 
   const int t = threadIdx.x;
   const int lane = t % kWave;
   const int wave = t / kWave;
-  const int wm = (wave / 4) * 128;
+  const int wm = (wave / 4) * (BM / 2);
   const int wn = (wave % 4) * 64;
   const int li = lane % 16, lk = lane / 16;
   constexpr bool kFp8 = is_fp8_block(KIND);
   constexpr bool kPlain = is_fp8_plain(KIND);
+  constexpr int kL = kAL + 4 + (kFp8 ? 1 : 0);  // copies per wave per K step
 
   // ---- per-lane global offsets of the direct-to-LDS loads (32-bit, checked
   // on the host). A: wave instruction i fills rows 8*(4*wave+i)..+7.
-  uint32_t a_off[4], b_off[4];
+  uint32_t a_off[kAL], b_off[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = 8 * (4 * wave + i) + lane / 8;
+  for (int i = 0; i < kAL; ++i) {
+    const int row = 8 * (kAL * wave + i) + lane / 8;
     const int64_t gm = min<int64_t>(m0 + row, p.m - 1);  // rows past M are never stored
     a_off[i] = static_cast<uint32_t>(gm * p.k + 16 * ((lane % 8) ^ a_swz(row)));
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
     const int krow = 4 * (4 * wave + i) + lane / 16;       // B: 4 k-rows per instruction
     b_off[i] = static_cast<uint32_t>(krow * p.n + n0 + 16 * ((lane % 16) ^ b_swz(krow)));
   }
@@ -384,11 +403,11 @@ gemm8_fast_kernel(Args p) {
 
   auto issue_loads = [&](int step, int buf) {
     const uint32_t k0 = static_cast<uint32_t>(step * kBK);
-    uint8_t* a_dst = sA + buf * kFBM * kFARow + (4 * wave) * 8 * kFARow;
+    uint8_t* a_dst = sA + buf * BM * kFARow + (kAL * wave) * 8 * kFARow;
     uint8_t* b_dst = sB + buf * kBK * kFBRow + (4 * wave) * 4 * kFBRow;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      dma_to_lds_off<16>(p.a, a_off[i] + k0, a_dst + i * 8 * kFARow);
+      if (i < kAL) dma_to_lds_off<16>(p.a, a_off[i] + k0, a_dst + i * 8 * kFARow);
       dma_to_lds_off<16>(p.b, b_off[i] + k0 * n32, b_dst + i * 4 * kFBRow);
     }
     if constexpr (kFp8) {  // block_k == 128: K step `step` is scale block `step`
@@ -397,10 +416,10 @@ gemm8_fast_kernel(Args p) {
     }
   };
 
-  f32x4 acc_o[8][4];
-  i32x4 acc_i[8][4];
+  f32x4 acc_o[kRB][4];
+  i32x4 acc_i[kRB][4];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < kRB; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       acc_o[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -425,13 +444,14 @@ gemm8_fast_kernel(Args p) {
     s_begin = split * per;
     steps = min(steps, s_begin + per);
   }
-  issue_loads(s_begin, 0);
-  __builtin_amdgcn_s_waitcnt(0);
+  for (int j = 0; j < NB - 1 && s_begin + j < steps; ++j) issue_loads(s_begin + j, j);
+  if (NB > 2 && s_begin + NB - 2 < steps) wait_vm<(NB - 2) * kL>();  // the first step landed
+  else __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   for (int s = s_begin; s < steps; ++s) {
-    const int cur = (s - s_begin) & 1;
-    if (s + 1 < steps) issue_loads(s + 1, cur ^ 1);
-    const uint8_t* a_src = sA + cur * kFBM * kFARow;
+    const int cur = (s - s_begin) % NB;
+    if (s + NB - 1 < steps) issue_loads(s + NB - 1, (cur + NB - 1) % NB);
+    const uint8_t* a_src = sA + cur * BM * kFARow;
     const uint8_t* b_src = sB + cur * kBK * kFBRow;
 
     // B fragment of n-block j: k rows kb0 + 0..KLEN-1 of columns wn+16j..+15
@@ -459,8 +479,8 @@ gemm8_fast_kernel(Args p) {
       const uint8_t* pa0 = a_src + (wm + li) * kFARow;
       const int ca0 = (lk ^ a_swz(li)) * 16, ca1 = ((4 + lk) ^ a_swz(li)) * 16;
       const float* sa0 = &sAs[cur * kFBM + wm + 4 * lk];
-      uint4 xa[8][2];
-      f32x4 scl[8];
+      uint4 xa[kRB][2];
+      f32x4 scl[kRB];
       auto read_a = [&](int i) {
         xa[i][0] = *reinterpret_cast<const uint4*>(pa0 + i * 16 * kFARow + ca0);
         xa[i][1] = *reinterpret_cast<const uint4*>(pa0 + i * 16 * kFARow + ca1);
@@ -477,15 +497,15 @@ gemm8_fast_kernel(Args p) {
         bs[j] = sBs[cur * kFBN + wn + 16 * j + li];
       }
       if (s > s_begin) {
-        promote16(acc_o[7][2], plast[0], UNIFORM_BS ? sclast : sclast * bslast[2]);
-        promote16(acc_o[7][3], plast[1], UNIFORM_BS ? sclast : sclast * bslast[3]);
+        promote16(acc_o[kRB - 1][2], plast[0], UNIFORM_BS ? sclast : sclast * bslast[2]);
+        promote16(acc_o[kRB - 1][3], plast[1], UNIFORM_BS ? sclast : sclast * bslast[3]);
       }
       __builtin_amdgcn_sched_barrier(0);
-      f32x4 part[32];
-      f32x4 sc[8];  // uniform b_scale: block scale; else the row scales
+      f32x4 part[4 * kRB];
+      f32x4 sc[kRB];  // uniform b_scale: block scale; else the row scales
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        if (i + 1 < 8) read_a(i + 1);
+      for (int i = 0; i < kRB; ++i) {
+        if (i + 1 < kRB) read_a(i + 1);
         const i32x8 fa = i32x8{(int)xa[i][0].x, (int)xa[i][0].y, (int)xa[i][0].z, (int)xa[i][0].w,
                                (int)xa[i][1].x, (int)xa[i][1].y, (int)xa[i][1].z, (int)xa[i][1].w};
         sc[i] = UNIFORM_BS ? scl[i] * bs[0] : scl[i];
@@ -502,9 +522,9 @@ gemm8_fast_kernel(Args p) {
           __builtin_amdgcn_sched_barrier(0);
         }
       }
-      plast[0] = part[30];
-      plast[1] = part[31];
-      sclast = sc[7];
+      plast[0] = part[4 * kRB - 2];
+      plast[1] = part[4 * kRB - 1];
+      sclast = sc[kRB - 1];
 #pragma unroll
       for (int j = 0; j < 4; ++j) bslast[j] = bs[j];
     } else if constexpr (kPlain) {
@@ -523,10 +543,10 @@ gemm8_fast_kernel(Args p) {
         fbp[j] = i32x8{q0[0], q0[1], q1[0], q1[1], q2[0], q2[1], q3[0], q3[1]};
       }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < kRB; ++i) {
         const i32x8 fa = i32x8{(int)xa0.x, (int)xa0.y, (int)xa0.z, (int)xa0.w,
                                (int)xa1.x, (int)xa1.y, (int)xa1.z, (int)xa1.w};
-        if (i + 1 < 8) {
+        if (i + 1 < kRB) {
           xa0 = *reinterpret_cast<const uint4*>(pa0 + (i + 1) * 16 * kFARow + ca0);
           xa1 = *reinterpret_cast<const uint4*>(pa0 + (i + 1) * 16 * kFARow + ca1);
         }
@@ -552,9 +572,9 @@ gemm8_fast_kernel(Args p) {
           fb[j] = i32x4{q0[0], q0[1], q1[0], q1[1]};
         }
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < kRB; ++i) {
           const i32x4 fa = i32x4{(int)xa.x, (int)xa.y, (int)xa.z, (int)xa.w};
-          if (i + 1 < 8) xa = read_a8(h, i + 1);
+          if (i + 1 < kRB) xa = read_a8(h, i + 1);
           else if (h == 0) xa = read_a8(1, 0);
 #pragma unroll
           for (int j = 0; j < 4; ++j)
@@ -564,13 +584,14 @@ gemm8_fast_kernel(Args p) {
     }
     // This wave's loads for step s+1 have landed (they were issued as inline
     // asm, so the compiler does not hold LDS reads of step s behind them).
-    __builtin_amdgcn_s_waitcnt(0);
+    if (NB > 2 && s + NB - 1 < steps) wait_vm<(NB - 2) * kL>();
+    else __builtin_amdgcn_s_waitcnt(0);
     barrier_no_wait();
   }
 
   if constexpr (kFp8) {
-    promote16(acc_o[7][2], plast[0], UNIFORM_BS ? sclast : sclast * bslast[2]);
-    promote16(acc_o[7][3], plast[1], UNIFORM_BS ? sclast : sclast * bslast[3]);
+    promote16(acc_o[kRB - 1][2], plast[0], UNIFORM_BS ? sclast : sclast * bslast[2]);
+    promote16(acc_o[kRB - 1][3], plast[1], UNIFORM_BS ? sclast : sclast * bslast[3]);
   }
 
   // ---- epilogue: lane holds rows wm+16i+4lk+r, column wn+16j+li ----
@@ -580,7 +601,7 @@ gemm8_fast_kernel(Args p) {
     for (int j = 0; j < 4; ++j) {
       const int64_t gn = n0 + wn + 16 * j + li;
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
+      for (int i = 0; i < kRB; ++i)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int64_t gm = m0 + wm + 16 * i + 4 * lk + r;
@@ -599,7 +620,7 @@ gemm8_fast_kernel(Args p) {
     float bsc = 0.f;
     if constexpr (KIND == INT8 || kPlain) bsc = p.b_per_channel ? p.b_scale[gn] : p.b_scale[0];
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < kRB; ++i)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int64_t gm = m0 + wm + 16 * i + 4 * lk + r;
@@ -623,7 +644,10 @@ gemm8_fast_kernel(Args p) {
   }
 }
 
-constexpr size_t kFastLds = 2 * kFBM * kFARow + 2 * kBK * kFBRow + 2 * (kFBM + kFBN) * sizeof(float);
+// LDS: A [NB][BM][128 B], B [NB][128][256 B], a_scale and b_scale [NB][256] fp32.
+constexpr size_t fast_lds(int bm) {
+  return fast_nb(bm) * (static_cast<size_t>(bm) * kFARow + kBK * kFBRow + (kFBM + kFBN) * sizeof(float));
+}
 
 // Any-shape fp8 blockwise fallback (one thread per output, reference order).
 template <typename Dec, typename Out>
@@ -704,25 +728,26 @@ inline bool fast_ok(const Args& p) {
          (reinterpret_cast<uintptr_t>(p.b) & 15u) == 0;
 }
 
-template <int KIND, typename Out, bool UBS, bool SPLIT>
+template <int KIND, typename Out, bool UBS, bool SPLIT, int BM>
 void launch_fast_kernel(const Args& p, int64_t wgs, hipStream_t s) {
+  constexpr size_t kLds = fast_lds(BM);
   // opt in to the LDS size once per process (thread-safe static initialization)
   static const bool configured = [] {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm8_fast_kernel<KIND, Out, UBS, SPLIT>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kFastLds));
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm8_fast_kernel<KIND, Out, UBS, SPLIT, BM>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kLds));
     return true;
   }();
   (void)configured;
-  hipLaunchKernelGGL((gemm8_fast_kernel<KIND, Out, UBS, SPLIT>), dim3(static_cast<unsigned>(wgs)),
-                     dim3(kFThreads), kFastLds, s, p);
+  hipLaunchKernelGGL((gemm8_fast_kernel<KIND, Out, UBS, SPLIT, BM>), dim3(static_cast<unsigned>(wgs)),
+                     dim3(kFThreads), kLds, s, p);
 }
 
 // Fewer tiles than CUs (M <= 512 at N = 7168): split K so tiles * splits
 // fills the 256 CUs (one 130 KB-LDS workgroup each), at least two K steps
 // per split; the splits' raw accumulators are summed in split order by
 // skinny_reduce_kernel, which also applies the epilogue.
-inline int fast_splits(const Args& p) {
-  const int64_t tiles = ((p.m + kFBM - 1) / kFBM) * ((p.n + kFBN - 1) / kFBN);
+inline int fast_splits(const Args& p, int bm) {
+  const int64_t tiles = ((p.m + bm - 1) / bm) * ((p.n + kFBN - 1) / kFBN);
   const int64_t steps = p.k / kBK;
   int64_t sp = std::min<int64_t>(256 / std::max<int64_t>(tiles, 1), steps / 2);
   if (sp <= 1 || (sp * p.m * p.n) >= (int64_t{1} << 31)) return 1;
@@ -730,19 +755,19 @@ inline int fast_splits(const Args& p) {
   return static_cast<int>((steps + per - 1) / per);  // every split gets >= 1 step
 }
 
-template <int KIND, typename Out, bool UBS>
+template <int KIND, typename Out, bool UBS, int BM>
 ks_status_t launch_fast_impl(Args p, hipStream_t s) {
-  const int64_t tiles = ((p.m + kFBM - 1) / kFBM) * ((p.n + kFBN - 1) / kFBN);
-  p.splits = fast_splits(p);
+  const int64_t tiles = ((p.m + BM - 1) / BM) * ((p.n + kFBN - 1) / kFBN);
+  p.splits = fast_splits(p, BM);
   if (p.splits == 1) {
-    launch_fast_kernel<KIND, Out, UBS, false>(p, tiles, s);
+    launch_fast_kernel<KIND, Out, UBS, false, BM>(p, tiles, s);
     return KS_SUCCESS;
   }
   Scratch sc;
   ks_status_t st = get_scratch(s, static_cast<size_t>(p.splits) * p.m * p.n, 0, &sc, "gemm8 split-K");
   if (st != KS_SUCCESS) return st;
   p.ws = sc.partial;
-  launch_fast_kernel<KIND, Out, UBS, true>(p, tiles * p.splits, s);
+  launch_fast_kernel<KIND, Out, UBS, true, BM>(p, tiles * p.splits, s);
   hipLaunchKernelGGL((skinny::skinny_reduce_kernel<KIND, Out>),
                      dim3(static_cast<unsigned>((p.m * p.n + 255) / 256)), dim3(256), 0, s, p);
   return KS_SUCCESS;
@@ -750,11 +775,14 @@ ks_status_t launch_fast_impl(Args p, hipStream_t s) {
 
 // A wave's 64 columns share one b_scale entry when block_n is a multiple of 64
 // (n0 and the wave offsets are multiples of 64).
+// M <= 64 takes 64-row tiles: a 256-row tile would spend three quarters of
+// its MFMAs and A copies on clamped rows past M.
 template <int KIND, typename Out>
 ks_status_t launch_fast(const Args& p, hipStream_t s) {
-  if ((KIND == FP8_E4M3 || KIND == FP8_E5M2) && p.block_n % 64 == 0)
-    return launch_fast_impl<KIND, Out, true>(p, s);
-  return launch_fast_impl<KIND, Out, false>(p, s);
+  const bool ubs = (KIND == FP8_E4M3 || KIND == FP8_E5M2) && p.block_n % 64 == 0;
+  if (p.m <= 64)
+    return ubs ? launch_fast_impl<KIND, Out, true, 64>(p, s) : launch_fast_impl<KIND, Out, false, 64>(p, s);
+  return ubs ? launch_fast_impl<KIND, Out, true, 256>(p, s) : launch_fast_impl<KIND, Out, false, 256>(p, s);
 }
 
 inline unsigned simple_grid(const Args& p) {

@@ -21,7 +21,7 @@ from tests.test_gemm8_gpu import (TOL, fp8_case, fp8_plain_case, run_fp8, run_fp
 pytestmark = pytest.mark.gpu
 
 SHAPES = [(17, 512, 2048), (100, 1024, 1536), (256, 2048, 4096), (300, 768, 1280),
-          (64, 256, 384)]
+          (64, 256, 384), (9, 768, 1024), (33, 512, 2560)]
 
 
 @pytest.mark.parametrize("m,n,k", SHAPES)
@@ -82,3 +82,16 @@ def test_splitk_w8a8_outputs_bitexact(out, bias):
     torch.cuda.synchronize()
     exp = O.round_to(O.w8a8_epilogue(O.w8a8_acc(a, b), a_s, b_s, bias_v, True, True), out)
     assert np.array_equal(H.from_dev_f32(c), exp)
+
+
+@pytest.mark.parametrize("m", [24, 64])
+def test_fast_64_row_tiles_unsplit(m):
+    # M <= 64 runs 64-row tiles; with N / 256 = 130 tiles no K split is taken
+    n, k = 33280, 256
+    a8, b8, a_s, b_s = fp8_case(m, n, k, seed=m + n)
+    got = run_fp8(a8, b8, a_s, b_s, 128, 128)
+    assert O.rel_err(got, O.fp8_blockwise_ref(a8, b8, a_s, b_s, 128, 128)) <= TOL
+    rng = np.random.default_rng(m)
+    a = rng.integers(-127, 128, (m, k)).astype(np.int8)
+    b = rng.integers(-127, 128, (k, n)).astype(np.int8)
+    assert np.array_equal(w8a8_acc_dev(a, b), O.w8a8_acc(a, b))
