@@ -326,7 +326,7 @@ __device__ inline int b_swz(int row) { return (row & 7) | ((((row >> 4) ^ (row >
 typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
 
 // LDS buffers of the fast kernel per tile height (see gemm8_fast_kernel).
-constexpr int fast_nb(int bm) { return bm == 64 ? 3 : 2; }
+constexpr int fast_nb(int bm) { return bm <= 128 ? 3 : 2; }
 
 // s_waitcnt vmcnt(N) only (expcnt and lgkmcnt left at their maxima).
 template <int N>
@@ -343,9 +343,9 @@ __device__ inline void wait_vm() {
 template <int KIND, typename Out, bool UNIFORM_BS, bool SPLIT, int BM>
 __global__ void __launch_bounds__(kFThreads)
 gemm8_fast_kernel(Args p) {
-  // BM = 256 or 64 rows per tile: each wave owns BM/2 rows = kRB 16-row
+  // BM = 256, 128 or 64 rows per tile: each wave owns BM/2 rows = kRB 16-row
   // blocks and issues kAL of the tile's 1 KB A copies per K step. NB LDS
-  // buffers: 64-row tiles leave room for three, so two steps of copies are in
+  // buffers: tiles of <= 128 rows leave room for three, so two steps of copies are in
   // flight (their splits run few steps, each bound by the copy round trip).
   constexpr int kRB = BM / 32, kAL = BM / 64, NB = fast_nb(BM);
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -775,13 +775,15 @@ ks_status_t launch_fast_impl(Args p, hipStream_t s) {
 
 // A wave's 64 columns share one b_scale entry when block_n is a multiple of 64
 // (n0 and the wave offsets are multiples of 64).
-// M <= 64 takes 64-row tiles: a 256-row tile would spend three quarters of
-// its MFMAs and A copies on clamped rows past M.
+// M <= 64 takes 64-row tiles and M <= 128 128-row tiles: a 256-row tile would
+// spend up to three quarters of its MFMAs and A copies on clamped rows past M.
 template <int KIND, typename Out>
 ks_status_t launch_fast(const Args& p, hipStream_t s) {
   const bool ubs = (KIND == FP8_E4M3 || KIND == FP8_E5M2) && p.block_n % 64 == 0;
   if (p.m <= 64)
     return ubs ? launch_fast_impl<KIND, Out, true, 64>(p, s) : launch_fast_impl<KIND, Out, false, 64>(p, s);
+  if (p.m <= 128)
+    return ubs ? launch_fast_impl<KIND, Out, true, 128>(p, s) : launch_fast_impl<KIND, Out, false, 128>(p, s);
   return ubs ? launch_fast_impl<KIND, Out, true, 256>(p, s) : launch_fast_impl<KIND, Out, false, 256>(p, s);
 }
 

@@ -21,7 +21,7 @@ from tests.test_gemm8_gpu import (TOL, fp8_case, fp8_plain_case, run_fp8, run_fp
 pytestmark = pytest.mark.gpu
 
 SHAPES = [(17, 512, 2048), (100, 1024, 1536), (256, 2048, 4096), (300, 768, 1280),
-          (64, 256, 384), (9, 768, 1024), (33, 512, 2560)]
+          (64, 256, 384), (9, 768, 1024), (33, 512, 2560), (65, 512, 1024), (128, 768, 2048)]
 
 
 @pytest.mark.parametrize("m,n,k", SHAPES)
