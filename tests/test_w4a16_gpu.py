@@ -151,6 +151,9 @@ def test_dq_split_k(dt):
     (200, 2048, 12288, 64, None, "f16", True),
     (256, 1024, 12288, 256, "int69", "bf16", True),
     (300, 512, 16384, 128, "int69", "f16", False),
+    # 96..191 tiles: the role-split kernel splits K (3 uneven splits here)
+    (100, 1024, 12288, 128, "int69", "bf16", True),
+    (70, 2048, 14336, 64, None, "f16", False),
 ])
 def test_dq_role_split_tiles(m, k, n, gs, zero_mode, dt, bias):
     # M > 64 with >= 192 tiles of 128 x 128: the role-split kernel (producer
