@@ -668,9 +668,12 @@ ks_status_t run(void* c_, const void* a_, const void* b_, const void* s_, const 
     // N=4096: 64 workgroups of 128x128 took 72.8 us).
     const bool wide = n % 128 == 0;
     auto wgs = [&](int bm, int bn) { return ((m + bm - 1) / bm) * ((n + bn - 1) / bn); };
-    // 128 x 128 tiles (the role-split kernel) from 96 tiles up, K-split below
-    // 192 (N = 14336, M = 96/128: 51 -> 43 us against 64 x 128 tiles).
-    if (m > 64 && wide && wgs(128, 128) >= 96) return launch_dq<T, 128, 128>(c, a, b, s, z, bias, m, n, k, gs, st);
+    // 128 x 128 tiles (the role-split kernel) from 32 tiles up, K-split below
+    // 192 workgroups (against 64 x 128 / 64 x 64 tiles: N = 14336 M = 96/128
+    // 51 -> 43 us; N = 8192 M = 128 40.8 -> 30.7 us; N = 4096 M = 256
+    // 40.4 -> 29.1 us, M = 65 24.9 -> 21.2 us; at 16 tiles, N = 2048 M = 96,
+    // 16.5 -> 18.4 us, so smaller grids keep the 64-row tiles).
+    if (m > 64 && wide && wgs(128, 128) >= 32) return launch_dq<T, 128, 128>(c, a, b, s, z, bias, m, n, k, gs, st);
     if (wide && wgs(64, 128) >= 192) return launch_dq<T, 64, 128>(c, a, b, s, z, bias, m, n, k, gs, st);
     if (m > 64 && wgs(128, 64) >= 192) return launch_dq<T, 128, 64>(c, a, b, s, z, bias, m, n, k, gs, st);
     return launch_dq<T, 64, 64>(c, a, b, s, z, bias, m, n, k, gs, st);

@@ -154,6 +154,8 @@ def test_dq_split_k(dt):
     # 96..191 tiles: the role-split kernel splits K (3 uneven splits here)
     (100, 1024, 12288, 128, "int69", "bf16", True),
     (70, 2048, 14336, 64, None, "f16", False),
+    (65, 1024, 4096, 128, "int69", "bf16", True),   # 32 tiles
+    (200, 2048, 4096, 64, None, "f16", False),      # 64 tiles
 ])
 def test_dq_role_split_tiles(m, k, n, gs, zero_mode, dt, bias):
     # M > 64 with >= 192 tiles of 128 x 128: the role-split kernel (producer
