@@ -775,14 +775,18 @@ ks_status_t launch_fast_impl(Args p, hipStream_t s) {
 
 // A wave's 64 columns share one b_scale entry when block_n is a multiple of 64
 // (n0 and the wave offsets are multiples of 64).
-// M <= 64 takes 64-row tiles and M <= 128 128-row tiles: a 256-row tile would
-// spend up to three quarters of its MFMAs and A copies on clamped rows past M.
+// M <= 64 takes 64-row tiles and M <= 384 128-row tiles: a 256-row tile would
+// spend up to three quarters of its MFMAs and A copies on clamped rows past M,
+// and the smaller tiles' 3-deep ring suits the few K steps of their splits
+// (fp8 blockwise N = K = 7168, M = 160/192/256: 36/37/41 -> 33.7/33.5/35.3 us;
+// M = 384 56.9 -> 54.1 us; at M = 512, 57.8 against 60.1 us, and at M = 2048
+// the 256-row tile is faster).
 template <int KIND, typename Out>
 ks_status_t launch_fast(const Args& p, hipStream_t s) {
   const bool ubs = (KIND == FP8_E4M3 || KIND == FP8_E5M2) && p.block_n % 64 == 0;
   if (p.m <= 64)
     return ubs ? launch_fast_impl<KIND, Out, true, 64>(p, s) : launch_fast_impl<KIND, Out, false, 64>(p, s);
-  if (p.m <= 128)
+  if (p.m <= 384)
     return ubs ? launch_fast_impl<KIND, Out, true, 128>(p, s) : launch_fast_impl<KIND, Out, false, 128>(p, s);
   return ubs ? launch_fast_impl<KIND, Out, true, 256>(p, s) : launch_fast_impl<KIND, Out, false, 256>(p, s);
 }
