@@ -135,3 +135,61 @@ def test_graph_replay_matches_eager(name):
         torch.cuda.synchronize()
         for o, r in zip(outs, ref):
             assert torch.equal(o.view(torch.uint8), r.view(torch.uint8)), f"replay {rep} differs"
+
+
+def test_scratch_growth_keeps_captured_graph_valid():
+    """A graph captured at a small shape keeps working after an eager call on
+    the same stream grows that stream's scratch: outgrown buffers are retired,
+    never freed, so the graph's split-K nodes still address live memory."""
+    g = torch.Generator(device=DEV).manual_seed(77)
+    small_fn, small_out = _w4(1, 4096, 4096, g)   # 16-split decode plane
+    big_fn, big_out = _w4(64, 4096, 14336, g)     # much larger ring-tile plane
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        small_fn()
+    torch.cuda.synchronize()
+    ref = small_out.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        small_fn()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(side):
+        big_fn()  # grows side's scratch; the small plane is retired
+    torch.cuda.synchronize()
+    big_ref = big_out.clone()
+    for rep in range(3):
+        small_out.view(torch.uint8).fill_(0xA5)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(small_out, ref), f"replay {rep} after growth differs"
+        with torch.cuda.stream(side):
+            big_fn()
+        torch.cuda.synchronize()
+        assert torch.equal(big_out, big_ref)
+
+
+def test_scratch_growth_refused_during_capture():
+    """A call that would have to grow scratch while its stream is being
+    captured returns KS_ERROR_INVALID_ARGUMENT (no sync, no allocation), and
+    the capture itself stays usable."""
+    from kernel_set._lib import KS_ERROR_INVALID_ARGUMENT, KernelSetError
+    g = torch.Generator(device=DEV).manual_seed(78)
+    fn, _ = _w4(1, 4096, 4096, g)
+    fresh = torch.cuda.Stream()  # no scratch yet for this stream
+    graph = torch.cuda.CUDAGraph()
+    err = None
+    with torch.cuda.stream(fresh):
+        graph.capture_begin()
+        try:
+            fn()
+        except KernelSetError as e:
+            err = e
+        finally:
+            graph.capture_end()
+    torch.cuda.synchronize()
+    assert err is not None and err.status == KS_ERROR_INVALID_ARGUMENT
+    assert "being captured" in str(err)
+    with torch.cuda.stream(fresh):
+        fn()  # eager: allocates normally
+    torch.cuda.synchronize()
