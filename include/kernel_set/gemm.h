@@ -41,6 +41,19 @@ KS_API ks_status_t ks_gemm_w4a16(void* c, const void* a, const void* b_packed,
                                  int64_t k, int group_size, ks_dtype_t dtype,
                                  ks_stream_t stream);
 
+/* No counterpart in the reference. ks_gemm_w4a16 with the same arguments and
+ * the same result bits, for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc): split-K
+ * partials live in a fixed 16 MiB per-device array instead of library-
+ * allocated scratch, and the call never allocates. A shape that needs more
+ * returns KS_ERROR_INVALID_ARGUMENT. Calls that overlap on one device (other
+ * streams, other threads) race on that array. */
+KS_API ks_status_t ks_gemm_w4a16_noalloc(void* c, const void* a, const void* b_packed,
+                                         const void* scales, const void* zeros,
+                                         const void* bias, int64_t m, int64_t n,
+                                         int64_t k, int group_size, ks_dtype_t dtype,
+                                         ks_stream_t stream);
+
 /* Replaces reference gemm.h:60-77 (kernels/src/gemm/gemm_fp8.cu:206-290).
  * fp8 A [M,K] x fp8 B [K,N] (both e4m3 or both e5m2, fp8_dtype), fp32
  * accumulation over all of K, then C = (acc * a_s) * b_s with a_scale fp32 [M]

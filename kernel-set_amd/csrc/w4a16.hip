@@ -38,6 +38,8 @@
 #include "w4a16_dec.hpp"
 #include "workspace.hpp"
 
+#include <mutex>
+
 namespace ks {
 namespace w4a16 {
 
@@ -716,15 +718,51 @@ ks_status_t run(void* c_, const void* a_, const void* b_, const void* s_, const 
   return KS_SUCCESS;
 }
 
+// ---- no-allocation variant: fixed per-device scratch --------------------
+// The split partial planes of every ks_gemm_w4a16 path come from this array
+// instead of library-allocated memory. Each device that the library runs on
+// holds one copy until the process ends. Host code must never pass the
+// symbol itself to a kernel (it names a host-side shadow): the device address
+// comes from hipGetSymbolAddress, once per device.
+constexpr size_t kNoAllocScratchBytes = size_t{16} << 20;
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+std::once_flag g_scratch_once[kMaxDevices];
+float* g_scratch_ptr[kMaxDevices];
+hipError_t g_scratch_err[kMaxDevices];
+
+// Device address of this device's `scratch`, resolved on the first call on
+// the device (with that device current).
+ks_status_t noalloc_scratch(float** out) {
+  int dev = 0;
+  ks_status_t st = check_hip(hipGetDevice(&dev), "ks_gemm_w4a16_noalloc");
+  if (st != KS_SUCCESS) return st;
+  if (dev < 0 || dev >= kMaxDevices) {
+    set_last_error("ks_gemm_w4a16_noalloc: device ordinal beyond the supported 64");
+    return KS_ERROR_INVALID_ARGUMENT;
+  }
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* p = nullptr;
+    g_scratch_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch_ptr[dev] = g_scratch_err[dev] == hipSuccess ? static_cast<float*>(p) : nullptr;
+  });
+  if (g_scratch_err[dev] != hipSuccess || g_scratch_ptr[dev] == nullptr)
+    return check_hip(g_scratch_err[dev] != hipSuccess ? g_scratch_err[dev] : hipErrorInvalidSymbol,
+                     "ks_gemm_w4a16_noalloc: hipGetSymbolAddress(scratch)");
+  *out = g_scratch_ptr[dev];
+  return KS_SUCCESS;
+}
+
 }  // namespace w4a16
 }  // namespace ks
 
 extern "C" {
 
-ks_status_t ks_gemm_w4a16(void* c, const void* a, const void* b_packed,
-                          const void* scales, const void* zeros, const void* bias,
-                          int64_t m, int64_t n, int64_t k, int group_size,
-                          ks_dtype_t dtype, ks_stream_t stream) {
+static ks_status_t gemm_w4a16_body(void* c, const void* a, const void* b_packed,
+                                   const void* scales, const void* zeros, const void* bias,
+                                   int64_t m, int64_t n, int64_t k, int group_size,
+                                   ks_dtype_t dtype, ks_stream_t stream) {
   KS_REQUIRE_PTR(c);
   KS_REQUIRE_PTR(a);
   KS_REQUIRE_PTR(b_packed);
@@ -746,6 +784,28 @@ ks_status_t ks_gemm_w4a16(void* c, const void* a, const void* b_packed,
   if (r != KS_SUCCESS) return r;
   KS_LAUNCH_STATUS("ks_gemm_w4a16");
   return KS_SUCCESS;
+}
+
+ks_status_t ks_gemm_w4a16(void* c, const void* a, const void* b_packed,
+                          const void* scales, const void* zeros, const void* bias,
+                          int64_t m, int64_t n, int64_t k, int group_size,
+                          ks_dtype_t dtype, ks_stream_t stream) {
+  return gemm_w4a16_body(c, a, b_packed, scales, zeros, bias, m, n, k, group_size, dtype, stream);
+}
+
+// Same kernels and bits as ks_gemm_w4a16; split partials go to the fixed
+// per-device `scratch` array, so the call never allocates. Calls that overlap
+// on one device race on that array.
+ks_status_t ks_gemm_w4a16_noalloc(void* c, const void* a, const void* b_packed,
+                                  const void* scales, const void* zeros, const void* bias,
+                                  int64_t m, int64_t n, int64_t k, int group_size,
+                                  ks_dtype_t dtype, ks_stream_t stream) {
+  float* ptr = nullptr;
+  ks_status_t r = ks::w4a16::noalloc_scratch(&ptr);
+  if (r != KS_SUCCESS) return r;
+  ks::ScratchOverride use(ptr, ks::w4a16::kNoAllocScratchBytes / sizeof(float), nullptr, 0,
+                          "16 MiB");
+  return gemm_w4a16_body(c, a, b_packed, scales, zeros, bias, m, n, k, group_size, dtype, stream);
 }
 
 }  // extern "C"

@@ -146,6 +146,7 @@ _decl("ks_memset_device", [_VP, _I, c_size_t, _VP])
 # gemm.h
 _decl("ks_gemm_w8a8", [_VP, _VP, _VP, _F32P, _F32P, _VP, _I64, _I64, _I64, _I, _I, _I, _VP])
 _decl("ks_gemm_w4a16", [_VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I, _I, _VP])
+_decl("ks_gemm_w4a16_noalloc", [_VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I, _I, _VP])
 _decl("ks_gemm_fp8", [_VP, _VP, _VP, _F32P, _F32P, _I64, _I64, _I64, _I, _I, _I, _I, _VP])
 _decl("ks_gemm_fp8_blockwise",
       [_VP, _VP, _VP, _F32P, _F32P, _I64, _I64, _I64, _I, _I, _I, _I, _VP])

@@ -12,7 +12,7 @@ from ._lib import check, lib
 from ._tensor import TensorLike, _is_tensor, default_stream, dtype_to_ks, infer_dtype, ptr
 from .enums import QuantMode
 
-__all__ = ["gemm_w8a8", "gemm_w4a16", "gemm_fp8", "gemm_fp8_blockwise"]
+__all__ = ["gemm_w8a8", "gemm_w4a16", "gemm_w4a16_noalloc", "gemm_fp8", "gemm_fp8_blockwise"]
 
 _F32P = POINTER(c_float)
 
@@ -77,6 +77,23 @@ def gemm_w4a16(c: TensorLike, a: TensorLike, b_packed: TensorLike, scales: Tenso
         ptr(scales, name="scales"), ptr(zeros, name="zeros"), ptr(bias, name="bias"),
         int(m), int(n), int(k), int(group_size), dt, default_stream(stream, a)),
         "ks_gemm_w4a16")
+    return c
+
+
+def gemm_w4a16_noalloc(c: TensorLike, a: TensorLike, b_packed: TensorLike, scales: TensorLike,
+                       zeros: TensorLike, m: int, n: int, k: int, group_size: int,
+                       bias: TensorLike = None, dtype: Optional[int] = None,
+                       stream: TensorLike = None) -> TensorLike:
+    """Extension (no reference counterpart): :func:`gemm_w4a16` with the same
+    bits, for callers that cannot allocate. Split-K partials use a fixed
+    16 MiB per-device array; larger needs raise ``KS_ERROR_INVALID_ARGUMENT``.
+    Calls that overlap on one device race on that array."""
+    dt = infer_dtype(a, dtype)
+    check(lib.ks_gemm_w4a16_noalloc(
+        ptr(c, name="c"), ptr(a, name="a"), ptr(b_packed, name="b_packed"),
+        ptr(scales, name="scales"), ptr(zeros, name="zeros"), ptr(bias, name="bias"),
+        int(m), int(n), int(k), int(group_size), dt, default_stream(stream, a)),
+        "ks_gemm_w4a16_noalloc")
     return c
 
 
