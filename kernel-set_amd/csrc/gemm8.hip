@@ -377,18 +377,25 @@ gemm8_fast_kernel(Args p) {
   constexpr int kL = kAL + 4 + (kFp8 ? 1 : 0);  // copies per wave per K step
 
   // ---- per-lane global offsets of the direct-to-LDS loads (32-bit, checked
-  // on the host). A: wave instruction i fills rows 8*(4*wave+i)..+7.
-  uint32_t a_off[kAL], b_off[4];
+  // on the host). A: wave instruction i fills rows 8*(kAL*wave+i)..+7 (rows
+  // past M are clamped, never stored). B: wave instruction i fills k-rows
+  // 4*(4*wave+i)..+3 from a wave-uniform base; the lane's chunk swizzle
+  // depends on i only through its parity, so two per-lane offsets serve all
+  // four.
+  uint32_t a_off[kAL];
 #pragma unroll
   for (int i = 0; i < kAL; ++i) {
     const int row = 8 * (kAL * wave + i) + lane / 8;
-    const int64_t gm = min<int64_t>(m0 + row, p.m - 1);  // rows past M are never stored
+    const int64_t gm = min<int64_t>(m0 + row, p.m - 1);
     a_off[i] = static_cast<uint32_t>(gm * p.k + 16 * ((lane % 8) ^ a_swz(row)));
   }
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const uint8_t* b_sb = p.b + static_cast<int64_t>(16 * wave_u) * p.n + n0;
+  uint32_t b_v[2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int krow = 4 * (4 * wave + i) + lane / 16;       // B: 4 k-rows per instruction
-    b_off[i] = static_cast<uint32_t>(krow * p.n + n0 + 16 * ((lane % 16) ^ b_swz(krow)));
+  for (int e = 0; e < 2; ++e) {
+    const int krow = 4 * (4 * wave + e) + lane / 16;
+    b_v[e] = static_cast<uint32_t>((lane / 16) * p.n + 16 * ((lane % 16) ^ b_swz(krow)));
   }
   const uint32_t n32 = static_cast<uint32_t>(p.n);
   // scales: waves 0-3 fetch a_scale of rows 64*wave+lane, waves 4-7 b_scale
@@ -401,20 +408,33 @@ gemm8_fast_kernel(Args p) {
     s_step = (wave < 4) ? 1 : p.nnb;
   }
 
-  auto issue_loads = [&](int step, int buf) {
+  // Copy q (0 <= q < kL) of K step `step` into LDS buffer `buf`: the kAL A
+  // copies, then the four B copies, then (fp8 blockwise) the scale vector.
+  auto issue_one = [&](int q, int step, int buf) {
     const uint32_t k0 = static_cast<uint32_t>(step * kBK);
-    uint8_t* a_dst = sA + buf * BM * kFARow + (kAL * wave) * 8 * kFARow;
-    uint8_t* b_dst = sB + buf * kBK * kFBRow + (4 * wave) * 4 * kFBRow;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (i < kAL) dma_to_lds_off<16>(p.a, a_off[i] + k0, a_dst + i * 8 * kFARow);
-      dma_to_lds_off<16>(p.b, b_off[i] + k0 * n32, b_dst + i * 4 * kFBRow);
-    }
-    if constexpr (kFp8) {  // block_k == 128: K step `step` is scale block `step`
-      float* s_dst = (wave < 4) ? sAs + buf * kFBM + 64 * wave : sBs + buf * kFBN + 64 * (wave - 4);
+    if (q < kAL) {
+      uint8_t* a_dst = sA + buf * BM * kFARow + (kAL * wave_u) * 8 * kFARow;
+      dma_to_lds_off<16>(p.a, a_off[q] + k0, a_dst + q * 8 * kFARow);
+    } else if (q < kAL + 4) {
+      const int i = q - kAL;
+      uint8_t* b_dst = sB + buf * kBK * kFBRow + (4 * wave_u) * 4 * kFBRow;
+      dma_to_lds_off<16>(b_sb + i * 4 * p.n, b_v[i & 1] + k0 * n32, b_dst + i * 4 * kFBRow);
+    } else if constexpr (kFp8) {  // block_k == 128: K step `step` is scale block `step`
+      float* s_dst = (wave_u < 4) ? sAs + buf * kFBM + 64 * wave_u : sBs + buf * kFBN + 64 * (wave_u - 4);
       dma_to_lds<4>(s_src + step * s_step, s_dst);
     }
   };
+  auto issue_loads = [&](int step, int buf) {
+#pragma unroll
+    for (int q = 0; q < kL; ++q) issue_one(q, step, buf);
+  };
+  // In the main loop the copies of step s+NB-1 are issued kDmaPer at a time
+  // at the head of the first row blocks, after the step's B-fragment reads:
+  // issuing all of them at the step start stalled every wave on the copy
+  // queue before its first MFMA (fp8 blockwise M=2048 N=K=7168: 141-146 ->
+  // 124-127 us).
+  constexpr int kDmaPer = 5;
+  static_assert(kDmaPer * kRB >= kL, "every copy gets a row block");
 
   f32x4 acc_o[kRB][4];
   i32x4 acc_i[kRB][4];
@@ -450,7 +470,15 @@ gemm8_fast_kernel(Args p) {
   __syncthreads();
   for (int s = s_begin; s < steps; ++s) {
     const int cur = (s - s_begin) % NB;
-    if (s + NB - 1 < steps) issue_loads(s + NB - 1, (cur + NB - 1) % NB);
+    const bool dma_now = s + NB - 1 < steps;
+    const int dma_step = s + NB - 1, dma_buf = (cur + NB - 1) % NB;
+    auto issue_group = [&](int i) {  // row block i's share of the step's copies
+      if (dma_now) {
+#pragma unroll
+        for (int q = kDmaPer * i; q < kDmaPer * (i + 1); ++q)
+          if (q < kL) issue_one(q, dma_step, dma_buf);
+      }
+    };
     const uint8_t* a_src = sA + cur * BM * kFARow;
     const uint8_t* b_src = sB + cur * kBK * kFBRow;
 
@@ -505,6 +533,7 @@ gemm8_fast_kernel(Args p) {
       f32x4 sc[kRB];  // uniform b_scale: block scale; else the row scales
 #pragma unroll
       for (int i = 0; i < kRB; ++i) {
+        issue_group(i);
         if (i + 1 < kRB) read_a(i + 1);
         const i32x8 fa = i32x8{(int)xa[i][0].x, (int)xa[i][0].y, (int)xa[i][0].z, (int)xa[i][0].w,
                                (int)xa[i][1].x, (int)xa[i][1].y, (int)xa[i][1].z, (int)xa[i][1].w};
@@ -544,6 +573,7 @@ gemm8_fast_kernel(Args p) {
       }
 #pragma unroll
       for (int i = 0; i < kRB; ++i) {
+        issue_group(i);
         const i32x8 fa = i32x8{(int)xa0.x, (int)xa0.y, (int)xa0.z, (int)xa0.w,
                                (int)xa1.x, (int)xa1.y, (int)xa1.z, (int)xa1.w};
         if (i + 1 < kRB) {
@@ -573,6 +603,7 @@ gemm8_fast_kernel(Args p) {
         }
 #pragma unroll
         for (int i = 0; i < kRB; ++i) {
+          if (h == 0) issue_group(i);
           const i32x4 fa = i32x4{(int)xa.x, (int)xa.y, (int)xa.z, (int)xa.w};
           if (i + 1 < kRB) xa = read_a8(h, i + 1);
           else if (h == 0) xa = read_a8(1, 0);
