@@ -11,14 +11,17 @@ blockwise GEMM and its 1x128 activation quantizer (config 3, the second half of
 the metric; plus the same GEMM at decode M = 1 and M = 64 with cold weights), the W4A16 sweep (config 2), W8A8 (config 4) and the MoE grouped
 W4A16 GEMM (config 5).
 
-Timing: calls are captured into a HIP graph (so host launch overhead is not
-measured) and replayed; HIP events recorded on the replay stream bracket
-exactly the timed calls, after untimed warm-up replays. Time per call =
-elapsed / calls.
+Timing: exactly --steps calls are captured into one HIP graph (so host launch
+overhead is not measured) and replayed once after untimed warm-up replays that
+cycle every rotated buffer set; HIP events recorded on the replay stream
+bracket exactly the timed calls. Time per call = elapsed / steps. The
+MFMA-bound secondary lines time max(32, min(steps, 64)) calls.
 
-cpu_baseline: the oracle's restatement of the reference's torch CPU path
-(dequantize, then fp32 matmul; bench.py:1274-1285 of the reference) on the
-host cores, on a bounded sample (repetitions of the headline problem).
+cpu_baseline: the reference bench's torch CPU path (benchmarks/bench.py
+:1274-1285 W4A16, :1434-1502 fp8 blockwise: dequantize, then fp32 matmul) on
+the host cores with torch's thread count stated, each half timed separately
+(median of >= 3 after a warm-up); W4A16 at the headline shape and fp8
+blockwise at the config 3 shape.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only headline]
 """
@@ -53,40 +56,57 @@ class Timer:
         self.stream = torch.cuda.Stream()
         self.graph = graph
 
-    def run(self, fn, rotate, steps, warmup, min_per_graph=64):
-        """fn(i) issues call i on buffer set i (i < rotate). Each graph holds at
-        least `min_per_graph` calls so graph-launch overhead is amortized.
+    def run(self, fn, rotate, steps, warmup):
+        """Times exactly `steps` calls. fn(i) issues call i on buffer set i
+        (i < rotate). The timed graph holds calls 0..steps-1 on sets i % rotate;
+        a warm-up graph replays every set once in order (at least `warmup`
+        calls) right before it, so set 0, the first timed one, was last touched
+        `rotate` calls earlier (cold in HBM when the sets outgrow the MALL).
+        At least 3 ms of warm-up replays are queued ahead of the start event,
+        so the timed replay starts on a busy, full-clock GPU with no host gap.
         Returns (ms per call, calls timed)."""
         torch = self.torch
-        per_graph = max(rotate, min_per_graph)
         inner = fn
         fn = lambda i: inner(i % rotate)  # noqa: E731
         with torch.cuda.stream(self.stream):
-            for i in range(per_graph):  # eager warm-up: allocates library scratch
+            for i in range(rotate):  # eager warm-up: allocates library scratch
                 fn(i)
         torch.cuda.synchronize()
         if not self.graph:
             return self._run_eager(fn, steps, warmup)
+        g_warm = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g_warm, stream=self.stream):
+            for i in range(rotate):
+                fn(i)
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=self.stream):
-            for i in range(per_graph):
+            for i in range(steps):
                 fn(i)
-        replays = max(1, -(-steps // per_graph))
         with torch.cuda.stream(self.stream):
-            for _ in range(max(1, -(-warmup // per_graph))):
-                g.replay()
-            torch.cuda.synchronize()
+            g.replay()  # first replay of a graph carries one-time setup
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            g_warm.replay()
+            e1.record()
+        torch.cuda.synchronize()
+        warm_ms = max(e0.elapsed_time(e1), 1e-3)
+        # Keep >= 3 ms of warm-up work queued ahead of the start event (and at
+        # least `warmup` calls), so the GPU is busy at full clock while the
+        # host enqueues the timed replay: no idle gap, no clock ramp inside it.
+        reps = max(-(-warmup // rotate), int(3.0 / warm_ms) + 1)
+        with torch.cuda.stream(self.stream):
+            for _ in range(reps):
+                g_warm.replay()
             start = torch.cuda.Event(enable_timing=True)
             end = torch.cuda.Event(enable_timing=True)
             start.record()
-            for _ in range(replays):
-                g.replay()
+            g.replay()
             end.record()
         torch.cuda.synchronize()
-        calls = replays * per_graph
-        ms = start.elapsed_time(end) / calls
-        del g
-        return ms, calls
+        ms = start.elapsed_time(end) / steps
+        del g, g_warm
+        return ms, steps
 
     def _run_eager(self, fn, steps, warmup):
         """Plain launches, each call bracketed by its own event pair on the
@@ -176,43 +196,71 @@ def wl_quant_group(torch, ks, H, rotate):
     return fn, rotate, nbytes, 0.0
 
 
-def wl_fp8_gemm(torch, ks, H):
-    import oracle as O
+def config3_activations(torch, ks, seed=2048, m=2048, k=7168):
+    """BASELINE config 3 activations: bf16 [M, K] ~N(0,1) with 0.1% of the
+    entries x50, quantized by ks_quantize_fp8_group (1x128 e4m3fn)."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    x = torch.randn(m, k, device="cuda", generator=g)
+    idx = torch.randperm(m * k, device="cuda", generator=g)[: (m * k) // 1000]
+    x.view(-1)[idx] *= 50.0
+    x = x.to(torch.bfloat16)
+    a8, a_s = ks.dispatch.per_token_group_quant(x, group_size=128)
+    return x, a8, a_s
+
+
+def block_quant_weight(torch, k, n, seed, bk=128, bn=128):
+    """BASELINE config 3 weights: fp32 [K, N] ~N(0, 0.02), e4m3fn with one fp32
+    scale per (bk x bn) block, scale = max(amax / 448, 1e-12) (the reference
+    bench's recipe, benchmarks/bench.py:1434-1461)."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    w = torch.randn(k, n, device="cuda", generator=g) * 0.02
+    blk = w.view(k // bk, bk, n // bn, bn)
+    b_s = (blk.abs().amax(dim=(1, 3)) / 448.0).clamp_min(1e-12)
+    b8 = (blk / b_s[:, None, :, None]).view(k, n).to(torch.float8_e4m3fn)
+    return b8, b_s.contiguous()
+
+
+def wl_fp8_gemm(torch, ks, H, rotate=6):
+    """Config 3: activations from ks_quantize_fp8_group (warm: one 14.7 MB set),
+    block-quantized weights cold: `rotate` distinct 51 MB sets (308 MB at 6,
+    over the 256 MB MALL), so every call streams B from HBM."""
     m, n, k = 2048, 7168, 7168
-    rng = np.random.default_rng(7)
-    a8 = torch.from_numpy(O.fp8_encode(rng.standard_normal((m, k)).astype(np.float32) * 50)).cuda()
-    b8 = torch.from_numpy(O.fp8_encode(rng.standard_normal((k, n)).astype(np.float32) * 50)).cuda()
-    a_s = torch.from_numpy(rng.uniform(0.001, 0.01, (m, k // 128)).astype(np.float32)).cuda()
-    b_s = torch.from_numpy(rng.uniform(0.001, 0.01, (k // 128, n // 128)).astype(np.float32)).cuda()
-    a8 = a8.view(torch.float8_e4m3fn)
-    b8 = b8.view(torch.float8_e4m3fn)
+    _, a8, a_s = config3_activations(torch, ks)
+    ws = [block_quant_weight(torch, k, n, 100 + r) for r in range(rotate)]
     out = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
 
     def fn(i):
+        b8, b_s = ws[i]
         ks.gemm.gemm_fp8_blockwise(out, a8, b8, a_s, b_s, m, n, k)
 
-    nbytes = m * k + k * n + m * n * 2 + a_s.numel() * 4 + b_s.numel() * 4
-    return fn, 8, nbytes, 2.0 * m * n * k
+    nbytes = m * k + k * n + m * n * 2 + a_s.numel() * 4 + ws[0][1].numel() * 4
+    return fn, rotate, nbytes, 2.0 * m * n * k
 
 
-def wl_fp8_plain(torch, ks, H):
-    """ks_gemm_fp8: per-token x per-channel scaled fp8 GEMM at the config 3 shape."""
-    import oracle as O
+def wl_fp8_plain(torch, ks, H, rotate=6):
+    """ks_gemm_fp8 at the config 3 shape: the same activations quantized per
+    token (ks_quantize_fp8), weights ~N(0, 0.02) quantized per output channel;
+    weights cold as in wl_fp8_gemm."""
     m, n, k = 2048, 7168, 7168
-    rng = np.random.default_rng(9)
-    a8 = torch.from_numpy(O.fp8_encode(rng.standard_normal((m, k)).astype(np.float32) * 50)).cuda()
-    b8 = torch.from_numpy(O.fp8_encode(rng.standard_normal((k, n)).astype(np.float32) * 50)).cuda()
-    a_s = torch.from_numpy(rng.uniform(0.001, 0.01, m).astype(np.float32)).cuda()
-    b_s = torch.from_numpy(rng.uniform(0.001, 0.01, n).astype(np.float32)).cuda()
-    a8 = a8.view(torch.float8_e4m3fn)
-    b8 = b8.view(torch.float8_e4m3fn)
+    x, _, _ = config3_activations(torch, ks)
+    a8 = torch.empty(m, k, device="cuda", dtype=torch.float8_e4m3fn)
+    a_s = torch.empty(m, device="cuda", dtype=torch.float32)
+    ks.quant.quantize_fp8(a8, a_s, x, m, k, mode=1)  # KS_QUANT_PER_TOKEN
+    ws = []
+    for r in range(rotate):
+        g = torch.Generator(device="cuda").manual_seed(200 + r)
+        w = torch.randn(k, n, device="cuda", generator=g) * 0.02
+        b_s = (w.abs().amax(dim=0) / 448.0).clamp_min(1e-12)
+        ws.append(((w / b_s).to(torch.float8_e4m3fn), b_s.contiguous()))
+        del w
     out = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
 
     def fn(i):
+        b8, b_s = ws[i]
         ks.gemm.gemm_fp8(out, a8, b8, a_s, b_s, m, n, k)
 
     nbytes = m * k + k * n + m * n * 2 + (m + n) * 4
-    return fn, 8, nbytes, 2.0 * m * n * k
+    return fn, rotate, nbytes, 2.0 * m * n * k
 
 
 def wl_fp8_skinny(torch, ks, H, m, rotate=6):
@@ -280,34 +328,93 @@ def wl_moe(torch, ks, H, K, N, rotate):
     return fn, rotate, nbytes, 2.0 * rows * N * K
 
 
-def cpu_baseline_w4a16(H, m, k, n, gs, budget_s=10.0):
-    """Oracle restatement of the reference torch CPU path on host cores."""
-    import oracle as O
-    a, codes, s, z = H.w4a16_inputs(m, k, n, gs, "fixed8", 0)
-    b = O.pack_k2_uint8(codes)
-    av, sv, zv = O.round_bf16(a), O.round_bf16(s), O.round_bf16(z)
-    O.w4a16_ref(av, b, sv, zv, gs, "bf16")  # warm-up
+def _median_time(fn, budget_s, min_reps=3):
+    fn()  # warm-up
     times = []
     t0 = time.perf_counter()
-    while time.perf_counter() - t0 < budget_s or len(times) < 3:
+    while len(times) < min_reps or time.perf_counter() - t0 < budget_s:
         t1 = time.perf_counter()
-        O.w4a16_ref(av, b, sv, zv, gs, "bf16")
+        fn()
         times.append(time.perf_counter() - t1)
-    med = float(np.median(times))
+    return float(np.median(times)), len(times)
+
+
+def cpu_baseline(torch, H, budget_s=10.0):
+    """The reference bench's torch CPU path (benchmarks/bench.py:1274-1285 for
+    W4A16, :1434-1502 for fp8 blockwise), timed on the host cores:
+    (i) dequantize the weights, (ii) fp32 matmul. Each piece is a median of
+    >= 3 timed repetitions after one warm-up, within `budget_s` seconds each."""
+    threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    # ---- W4A16, config 1 (M=1, K=N=4096, g=128, zeros 8) ----
+    m, k, n, gs = 1, 4096, 4096, 128
+    a, codes, s, z = H.w4a16_inputs(m, k, n, gs, "fixed8", 0)
+    import oracle as O
+    packed = torch.from_numpy(O.pack_k2_uint8(codes))
+    at = torch.from_numpy(a).to(torch.bfloat16)
+    st = torch.from_numpy(s).to(torch.bfloat16)
+    zt = torch.from_numpy(z).to(torch.bfloat16)
+    kk = torch.arange(k)
+    grp = kk // gs
+    odd = (kk & 1).view(k, 1).bool()
+    holder = {}
+
+    def dequant():
+        byte = packed[kk >> 1]
+        q = torch.where(odd, (byte >> 4) & 0xF, byte & 0xF).float()
+        holder["w"] = ((q - zt.float()[grp]) * st.float()[grp]).to(torch.bfloat16)
+
+    def matmul():
+        holder["c"] = (at.float() @ holder["w"].float()).to(torch.bfloat16)
+
+    t_dq, r_dq = _median_time(dequant, budget_s / 4)
+    t_mm, r_mm = _median_time(matmul, budget_s / 4)
     nbytes = (k // 2) * n + 2 * (k // gs) * n * 2 + m * k * 2 + m * n * 2
-    return {
-        "value": round(nbytes / med / 1e9, 4), "unit": "GB/s",
-        "cores": int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)),
-        "kind": "port",
-        "sample": (f"{len(times)} repetitions of W4A16 M={m} K={k} N={n} g={gs}: oracle "
-                   f"unpack + (q-z)*s -> bf16 + fp32 matmul (numpy BLAS), median "
-                   f"{med * 1e3:.2f} ms per call"),
+    out = {
+        "value": round(nbytes / (t_dq + t_mm) / 1e9, 4), "unit": "GB/s",
+        "cores": torch.get_num_threads(), "kind": "port",
+        "os_cpu_count": os.cpu_count(),
+        "sample": (f"torch CPU ({torch.get_num_threads()} threads) W4A16 M={m} K={k} N={n} g={gs}: "
+                   f"(i) K-packed int4 dequant -> bf16 [K,N] median {t_dq * 1e3:.3f} ms of {r_dq}, "
+                   f"(ii) fp32 matmul median {t_mm * 1e3:.3f} ms of {r_mm}; value = algorithmic "
+                   "bytes / (i + ii)"),
+        "w4a16_dequant_ms": round(t_dq * 1e3, 4), "w4a16_matmul_ms": round(t_mm * 1e3, 4),
     }
+    # ---- fp8 blockwise, config 3 shape (M=2048, N=K=7168, 1x128 / 128x128) ----
+    m, n, k = 2048, 7168, 7168
+    gen = torch.Generator().manual_seed(3)
+    a8 = (torch.randn(m, k, generator=gen) * 100).clamp(-448, 448).to(torch.float8_e4m3fn)
+    b8 = (torch.randn(k, n, generator=gen) * 100).clamp(-448, 448).to(torch.float8_e4m3fn)
+    a_s = torch.rand(m, k // 128, generator=gen) * 0.01 + 1e-4
+    b_s = torch.rand(k // 128, n // 128, generator=gen) * 1e-4 + 1e-5
+
+    def dequant8():
+        holder["ad"] = (a8.float().view(m, k // 128, 128) * a_s[:, :, None]).view(m, k)
+        holder["bd"] = (b8.float().view(k // 128, 128, n // 128, 128)
+                        * b_s[:, None, :, None]).view(k, n)
+
+    def matmul8():
+        holder["o8"] = (holder["ad"] @ holder["bd"]).to(torch.bfloat16)
+
+    t_dq8, r_dq8 = _median_time(dequant8, budget_s / 4)
+    t_mm8, r_mm8 = _median_time(matmul8, budget_s / 4)
+    fl = 2.0 * m * n * k
+    out["fp8_blockwise"] = {
+        "value": round(fl / (t_dq8 + t_mm8) / 1e12, 4), "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(), "kind": "port",
+        "sample": (f"torch CPU fp8 blockwise M={m} N={n} K={k}: (i) float(fp8) * scale for A and B "
+                   f"median {t_dq8 * 1e3:.1f} ms of {r_dq8}, (ii) fp32 matmul median "
+                   f"{t_mm8 * 1e3:.1f} ms of {r_mm8}"),
+        "dequant_ms": round(t_dq8 * 1e3, 2), "matmul_ms": round(t_mm8 * 1e3, 2),
+    }
+    return out
 
 
-def line(name, ms, calls, nbytes, flops, bound, peak_key=None):
+def line(name, ms, calls, nbytes, flops, bound, peak_key=None, note=None):
     d = {"us_per_call": round(ms * 1e3, 3), "calls": calls, "bytes": nbytes,
          "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 2)}
+    if note:
+        d["inputs"] = note
     if flops:
         d["TFLOP/s"] = round(flops / (ms * 1e-3) / 1e12, 2)
     if bound == "hbm":
@@ -400,16 +507,22 @@ def main():
     if only - {"headline"}:
         sec = {}
         steps = max(64, args.steps // 8)
+        n_mfma = max(32, min(args.steps, 64))  # timed calls per MFMA-bound line
         if "gemm8" in only:
             fn, per, nb, fl = wl_fp8_gemm(torch, ks, H)
-            ms2, c2 = T.run(fn, per, max(32, steps // 8), 8, min_per_graph=8)
-            sec["fp8_blockwise_gemm_M2048_N7168_K7168"] = line("fp8 gemm", ms2, c2, nb, fl, "mfma", "fp8")
+            ms2, c2 = T.run(fn, per, n_mfma, 12)
+            sec["fp8_blockwise_gemm_M2048_N7168_K7168"] = line(
+                "fp8 gemm", ms2, c2, nb, fl, "mfma", "fp8",
+                note="config 3: A = ks_quantize_fp8_group(bf16 N(0,1), 0.1% x50), warm; "
+                     "W ~N(0,0.02) 128x128 block-quantized, cold (6 rotated 51 MB sets)")
             fn, per, nb, fl = wl_fp8_plain(torch, ks, H)
-            ms2, c2 = T.run(fn, per, max(32, steps // 8), 8, min_per_graph=8)
-            sec["fp8_per_token_gemm_M2048_N7168_K7168"] = line("fp8 gemm per-token", ms2, c2, nb, fl, "mfma", "fp8")
+            ms2, c2 = T.run(fn, per, n_mfma, 12)
+            sec["fp8_per_token_gemm_M2048_N7168_K7168"] = line(
+                "fp8 gemm per-token", ms2, c2, nb, fl, "mfma", "fp8",
+                note="config 3 activations per-token quantized (warm); W per-channel, cold")
             for mm in (1, 64):  # decode / small batch: HBM-bound (B = 51 MB)
                 fn, per, nb, fl = wl_fp8_skinny(torch, ks, H, mm)
-                ms2, c2 = T.run(fn, per, max(64, steps // 4), 12, min_per_graph=24)
+                ms2, c2 = T.run(fn, per, max(64, steps // 4), 12)
                 sec[f"fp8_blockwise_gemm_M{mm}_N7168_K7168_cold"] = line(
                     f"fp8 gemm M={mm}", ms2, c2, nb, fl, "hbm")
         if "quant" in only:
@@ -426,7 +539,7 @@ def main():
             sec[f"w4a16_M{mm}_K4096_N14336_cold"] = d
         if "gemm8" in only:
             fn, per, nb, fl = wl_w8a8(torch, ks, H)
-            ms2, c2 = T.run(fn, per, max(32, steps // 8), 8, min_per_graph=8)
+            ms2, c2 = T.run(fn, per, n_mfma, 8)
             sec["w8a8_M4096_N4096_K4096"] = line("w8a8", ms2, c2, nb, fl, "mfma", "int8")
         for K_, N_, nm in (((2048, 1536, "gate_up"), (768, 2048, "down")) if "moe" in only else ()):
             fn, per, nb, fl = wl_moe(torch, ks, H, K_, N_, 4)
@@ -438,7 +551,7 @@ def main():
             result["fp8_gemm_tflops"] = fp8["TFLOP/s"]
             result["fp8_gemm_frac_of_peak"] = fp8["roofline_frac"]
 
-    result["cpu_baseline"] = cpu_baseline_w4a16(H, m, k, n, gs, args.cpu_budget)
+    result["cpu_baseline"] = cpu_baseline(torch, H, args.cpu_budget)
     print(json.dumps(result), flush=True)
 
 
