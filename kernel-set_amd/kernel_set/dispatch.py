@@ -9,6 +9,8 @@ fallback. Introspection helpers report that single provider.
 """
 from __future__ import annotations
 
+import weakref
+
 import torch
 
 from . import gemm as _gemm
@@ -52,12 +54,31 @@ def int8_gemm(a8, b8, a_scale, b_scale, *, out_dtype=None, **kw):
     return out
 
 
+# [N, K] fp8 weight -> its [K, N] copy, made once per weight tensor: keyed on
+# the tensor's identity (the entry is dropped when the weight is freed) and
+# revalidated against its storage pointer, shape, strides and in-place version.
+_KN_CACHE: dict = {}
+
+
+def _weight_kn(b8):
+    key = (b8.data_ptr(), tuple(b8.shape), tuple(b8.stride()), b8._version)
+    ent = _KN_CACHE.get(id(b8))
+    if ent is not None and ent[2]() is b8 and ent[0] == key:
+        return ent[1]
+    kn = b8.t().contiguous()
+    ident = id(b8)
+    _KN_CACHE[ident] = (key, kn, weakref.ref(b8, lambda _r, i=ident: _KN_CACHE.pop(i, None)))
+    return kn
+
+
 def fp8_gemm(a8, b8, a_scale, b_scale, *, out_dtype=None, **kw):
     """Scaled fp8 GEMM ``C = (a_scale (x) b_scale) * (a8 @ b8.T)``. ``b8`` is
     ``[N, K]`` (the NT weight layout of the reference's fp8_gemm providers,
     ``backends/_registry.py:427-442``); ``a_scale`` is ``[M]``/``[M,1]`` or one
     element, ``b_scale`` ``[N]``/``[1,N]`` or one element; default bf16 out.
-    ``ks_gemm_fp8`` takes B as ``[K, N]``, so ``b8`` is transposed once here."""
+    ``ks_gemm_fp8`` takes B as ``[K, N]``; the transposed copy is made on the
+    first call with a given weight tensor and reused while that tensor lives
+    unmodified, so steady-state calls move no extra weight bytes."""
     m, k = a8.shape
     n = b8.shape[0]
     out = torch.empty(m, n, device=a8.device, dtype=out_dtype or torch.bfloat16)
@@ -68,7 +89,7 @@ def fp8_gemm(a8, b8, a_scale, b_scale, *, out_dtype=None, **kw):
         raise ValueError(f"fp8_gemm: a_scale must have 1 or M={m} elements")
     if b_mode == QuantMode.PER_CHANNEL and b_scale.numel() != n:
         raise ValueError(f"fp8_gemm: b_scale must have 1 or N={n} elements")
-    b_kn = b8.t().contiguous()
+    b_kn = _weight_kn(b8)
     _gemm.gemm_fp8(out, a8, b_kn, a_scale.contiguous(), b_scale.contiguous(), m=m, n=n, k=k,
                    a_mode=a_mode, b_mode=b_mode, out_dtype=dtype_to_ks(out.dtype))
     return out

@@ -1,7 +1,9 @@
-"""GPU parity of the split-K form of the 256x256 8-bit GEMM kernel, taken
-when the output has fewer tiles than the chip has CUs (e.g. 17 <= M <= 512 at
-N = 7168): every split writes its raw accumulators to a partial plane and a
-second kernel sums them in split order, then applies the epilogue.
+"""GPU parity of the split-K form of the fast 8-bit GEMM kernel, taken when
+the output has fewer tiles than the chip has CUs (e.g. 9 <= M <= 512 at
+N = 7168). The row tile follows M: 64 rows for M <= 64, 128 rows for
+M <= 384, 256 rows above (all 256 columns wide). Every split writes its raw
+accumulators to a partial plane and a second kernel sums them in split order,
+then applies the epilogue.
 
 Bars as for the unsplit kernel: fp8 blockwise / plain fp8 max-rel <= 1e-2
 against the closed-form oracle and exact on integer-valued operands with unit

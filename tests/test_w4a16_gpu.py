@@ -158,9 +158,9 @@ def test_dq_split_k(dt):
     (200, 2048, 4096, 64, None, "f16", False),      # 64 tiles
 ])
 def test_dq_role_split_tiles(m, k, n, gs, zero_mode, dt, bias):
-    # M > 64 with >= 192 tiles of 128 x 128: the role-split kernel (producer
-    # waves copy and dequantize, consumer waves run the MFMAs); M not a
-    # multiple of 128 leaves a ragged last row tile.
+    # M > 64 with >= 32 tiles of 128 x 128 (K split below 192 workgroups): the
+    # role-split kernel (producer waves copy and dequantize, consumer waves run
+    # the MFMAs); M not a multiple of 128 leaves a ragged last row tile.
     check(m, k, n, gs, zero_mode=zero_mode, dt=dt, seed=m + gs, bias=bias)
 
 
