@@ -142,20 +142,28 @@ class Timer:
         return int(min(seconds, 1.0) * self._cyc_per_s)
 
 
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "w4a16_gemv_M1_K4096_N4096_hbm_bytes.md")
+PROFILES = os.path.join(ROOT, "profiles")
+HEADLINE_KEY = "w4a16_gemv_M1_K4096_N4096 (headline)"
 
 
 def measured_traffic():
-    """HBM bytes per headline call from the committed rocprofv3 PMC summary
-    (FETCH_SIZE and WRITE_SIZE per dispatch, scaled by a copy calibration)."""
+    """HBM bytes per call of each bench line, from the committed rocprofv3 PMC
+    summaries in profiles/ (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by a
+    copy calibration): lines `traffic_bytes_per_call[<line key>]: <bytes>`."""
+    out = {}
     try:
-        with open(TRAFFIC_FILE) as f:
-            for ln in f:
-                if ln.startswith("traffic_bytes_per_call:"):
-                    return int(ln.split(":", 1)[1].strip())
+        names = sorted(os.listdir(PROFILES))
     except OSError:
-        pass
-    return None
+        return out
+    for fn in names:
+        if not fn.endswith(".md"):
+            continue
+        with open(os.path.join(PROFILES, fn)) as f:
+            for ln in f:
+                if ln.startswith("traffic_bytes_per_call[") and "]:" in ln:
+                    key, val = ln[len("traffic_bytes_per_call["):].split("]:", 1)
+                    out[key] = int(float(val.strip()))
+    return out
 
 
 def rot_copies(t, n):
@@ -494,7 +502,7 @@ def main():
                    "device": dev_name},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(),
+                     "traffic": measured_traffic().get(HEADLINE_KEY),
                      "kernel": "ks_gemm_w4a16 call = ks::w4dec::dec_kernel + ks::w4a16::dec_reduce_kernel",
                      "bytes_per_launch": nbytes},
         "warm_cache": {"us_per_call": round(ms_warm * 1e3, 3),
@@ -545,6 +553,9 @@ def main():
             fn, per, nb, fl = wl_moe(torch, ks, H, K_, N_, 4)
             ms2, c2 = T.run(fn, per, steps, 16)
             sec[f"moe_w4a16_{nm}_E64_top8_T256_cold"] = line(f"moe {nm}", ms2, c2, nb, fl, "hbm")
+        traffic = measured_traffic()
+        for key, d in sec.items():
+            d["traffic"] = traffic.get(key)
         result["secondary"] = sec
         fp8 = sec.get("fp8_blockwise_gemm_M2048_N7168_K7168")
         if fp8:
