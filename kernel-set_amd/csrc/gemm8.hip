@@ -645,6 +645,52 @@ gemm8_fast_kernel(Args p) {
     }
     return;
   }
+  // 16-bit outputs: the tile is staged through LDS (the A/B buffers are free
+  // after the last step's barrier) and written as whole 512-byte row segments
+  // with 16-byte non-temporal stores, instead of 2-byte stores per lane
+  // (fp8 blockwise config 3: ~4 us of a ~115 us call). Row stride 528 B: the
+  // four rows one 2-byte LDS write touches land 16 banks apart.
+  if constexpr (sizeof(typename Out::storage) == 2 && KIND != INT8_RAW) {
+    constexpr int kRowB = 528;
+    static_assert(BM * kRowB <= NB * (BM * kFARow + kBK * kFBRow + (kFBM + kFBN) * 4), "staging fits");
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int col = wn + 16 * j + li;
+      const int64_t gn = n0 + col;
+      float bsc = 0.f;
+      if constexpr (KIND == INT8 || kPlain) bsc = p.b_per_channel ? p.b_scale[gn] : p.b_scale[0];
+#pragma unroll
+      for (int i = 0; i < kRB; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = wm + 16 * i + 4 * lk + r;
+          const int64_t gm = min<int64_t>(m0 + row, p.m - 1);  // rows past M are never stored
+          float v;
+          if constexpr (kPlain) {
+            const float as = p.a_per_token ? p.a_scale[gm] : p.a_scale[0];
+            v = __fmul_rn(__fmul_rn(acc_o[i][j][r], as), bsc);
+          } else if constexpr (kFp8) {
+            v = acc_o[i][j][r];
+          } else {
+            const float as = p.a_per_token ? p.a_scale[gm] : p.a_scale[0];
+            v = __fmul_rn(__fmul_rn(static_cast<float>(acc_i[i][j][r]), as), bsc);
+            if (p.bias)
+              v = __fadd_rn(v, elem<Out>::load(static_cast<const typename Out::storage*>(p.bias), gn));
+          }
+          *reinterpret_cast<uint16_t*>(smem + row * kRowB + 2 * col) = elem<Out>::from_f32(v);
+        }
+    }
+    __syncthreads();
+    uint16_t* outp = static_cast<uint16_t*>(p.out);
+#pragma unroll 4
+    for (int e = t; e < BM * 32; e += kFThreads) {
+      const int row = e >> 5, ch = e & 31;
+      const int64_t gm = m0 + row;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(smem + row * kRowB + 16 * ch);
+      if (gm < p.m) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(outp + gm * p.n + n0 + 8 * ch));
+    }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int64_t gn = n0 + wn + 16 * j + li;
