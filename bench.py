@@ -336,6 +336,33 @@ def wl_moe(torch, ks, H, K, N, rotate):
     return fn, rotate, nbytes, 2.0 * rows * N * K
 
 
+def wl_moe_dense(torch, ks, H, K, N, rotate):
+    """Dense grouped GEMM (ks_moe_grouped_gemm) at the config 5 routing and
+    shapes with bf16 weights ~N(0, 0.02) (the reference's dense form)."""
+    import oracle as O
+    E, T, top_k = 64, 256, 8
+    rng = np.random.default_rng(K + 1)
+    ids = O.moe_topk_ids(rng.standard_normal((T, E)).astype(np.float32), top_k)
+    row_src, offs = O.moe_group_rows(ids, E, 16)
+    a = np.zeros((len(row_src), K), np.float32)
+    live = row_src >= 0
+    a[live] = rng.standard_normal((int(live.sum()), K)).astype(np.float32)
+    at, _ = H.to_dev(a, "bf16")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(K)
+    bs = [(torch.randn(E, K, N, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+          for _ in range(rotate)]
+    offt = H.np_i32_dev(offs)
+    c = torch.empty(len(row_src), N, device="cuda", dtype=torch.bfloat16)
+    rows = int(live.sum())
+
+    def fn(i):
+        ks.moe.grouped_gemm(c, at, bs[i], offt, E, len(row_src), N, K)
+
+    nbytes = E * K * N * 2 + rows * K * 2 + rows * N * 2
+    return fn, rotate, nbytes, 2.0 * rows * N * K
+
+
 def _median_time(fn, budget_s, min_reps=3):
     fn()  # warm-up
     times = []
@@ -553,6 +580,10 @@ def main():
             fn, per, nb, fl = wl_moe(torch, ks, H, K_, N_, 4)
             ms2, c2 = T.run(fn, per, steps, 16)
             sec[f"moe_w4a16_{nm}_E64_top8_T256_cold"] = line(f"moe {nm}", ms2, c2, nb, fl, "hbm")
+        for K_, N_, nm in (((2048, 1536, "gate_up"), (768, 2048, "down")) if "moe" in only else ()):
+            fn, per, nb, fl = wl_moe_dense(torch, ks, H, K_, N_, 2)
+            ms2, c2 = T.run(fn, per, steps, 16)
+            sec[f"moe_dense_bf16_{nm}_E64_top8_T256_cold"] = line(f"moe dense {nm}", ms2, c2, nb, fl, "hbm")
         traffic = measured_traffic()
         for key, d in sec.items():
             d["traffic"] = traffic.get(key)

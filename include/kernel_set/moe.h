@@ -2,9 +2,9 @@
  * kernel-set (MI355X build) -- MoE routing around the grouped W4A16 GEMM.
  *
  * Same entry points, argument order and meaning as the reference's
- * include/kernel_set/moe.h:15-55 (gate -> permutation -> permute -> grouped
- * GEMM -> unpermute). The dense ks_moe_grouped_gemm is not part of this build;
- * the quantized grouped GEMM is ks_moe_grouped_gemm_w4a16 (moe_w4a16.h).
+ * include/kernel_set/moe.h:15-65 (gate -> permutation -> permute -> grouped
+ * GEMM -> unpermute). The quantized grouped GEMM is the extension
+ * ks_moe_grouped_gemm_w4a16 (moe_w4a16.h).
  *
  * Differences from the reference, all on the safe side of its contract:
  *   - ks_moe_compute_permutation is deterministic: inside each expert the pair
@@ -70,6 +70,18 @@ KS_API ks_status_t ks_moe_unpermute(void* out, const void* permuted,
                                     int64_t num_tokens, int top_k,
                                     int64_t hidden, ks_dtype_t dtype,
                                     ks_stream_t stream);
+
+/* Dense grouped GEMM: for each expert e,
+ * C[off_e:off_{e+1}] = A[off_e:off_{e+1}] @ B_e, fp32 accumulation, one
+ * rounding to dtype (f32, f16, bf16, f8e4m3, f8e5m2; A, B and C share it).
+ *   a [total_rows, k]; b [num_experts, k, n] (n contiguous); expert_offsets
+ *   [num_experts+1] int32 row boundaries; c [total_rows, n]. Rows outside
+ *   every expert's range are not written.
+ * Reference: include/kernel_set/moe.h:57-65, kernels/src/moe/moe_grouped_gemm.cu:136-198. */
+KS_API ks_status_t ks_moe_grouped_gemm(
+    void* c, const void* a, const void* b, const int32_t* expert_offsets,
+    int num_experts, int64_t total_rows, int64_t n, int64_t k,
+    ks_dtype_t dtype, ks_stream_t stream);
 
 KS_END_EXTERN_C
 

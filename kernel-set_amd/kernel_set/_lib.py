@@ -170,6 +170,7 @@ _decl("ks_moe_gate_sigmoid_group_topk",
 _decl("ks_moe_compute_permutation", [_I32P, _I32P, _I32P, _I64, _I, _I, _VP])
 _decl("ks_moe_permute", [_VP, _VP, _I32P, _I64, _I, _I64, _I, _VP])
 _decl("ks_moe_unpermute", [_VP, _VP, _I32P, _F32P, _I64, _I, _I64, _I, _VP])
+_decl("ks_moe_grouped_gemm", [_VP, _VP, _VP, _I32P, _I, _I64, _I64, _I64, _I, _VP])
 # moe_w4a16.h (extension)
 _decl("ks_moe_grouped_gemm_w4a16",
       [_VP, _VP, _VP, _VP, _VP, _I32P, _I, _I64, _I64, _I64, _I, _I, _VP])

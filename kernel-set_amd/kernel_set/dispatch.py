@@ -16,7 +16,6 @@ import torch
 from . import gemm as _gemm
 from . import moe as _moe
 from . import quant as _quant
-from ._lib import KS_ERROR_NOT_IMPLEMENTED, KernelSetError
 from ._tensor import dtype_to_ks
 from .enums import DType
 
@@ -122,18 +121,20 @@ def per_token_group_quant(x, *, group_size=128, fp8_dtype=None, **kw):
 
 def moe(a, b, expert_offsets, *, num_experts, n, k, scales=None, zeros=None,
         group_size=128, **kw):
-    """Grouped expert GEMM over CSR ``expert_offsets``. The native path is the
-    W4A16 grouped GEMM: ``b`` is uint8 ``[E, k/2, n]`` with ``scales``/``zeros``
-    ``[E, k/group_size, n]``. The dense-weight form of the reference is outside
-    this build and raises NOT_IMPLEMENTED."""
-    if scales is None or b.dtype != torch.uint8:
-        raise KernelSetError(KS_ERROR_NOT_IMPLEMENTED, "KS_ERROR_NOT_IMPLEMENTED",
-                             "dense grouped GEMM is not part of this build; pass packed "
-                             "int4 weights with scales=", "moe")
+    """Grouped expert GEMM over CSR ``expert_offsets``.
+
+    Dense form (the reference's kernel-set provider, ``_registry.py:1040-1046``):
+    ``b`` is ``[E, k, n]`` of ``a``'s dtype, ``scales`` is None. W4A16 form
+    (extension): ``b`` is uint8 ``[E, k/2, n]`` with ``scales``/``zeros``
+    ``[E, k/group_size, n]``. Returns ``C [total_rows, n]`` of ``a``'s dtype;
+    rows outside every expert's range are left as ``torch.empty`` made them."""
     total_rows = a.shape[0]
     c = torch.empty(total_rows, n, device=a.device, dtype=a.dtype)
-    _moe.grouped_gemm_w4a16(c, a, b, scales, zeros, expert_offsets, num_experts,
-                            total_rows, n, k, group_size=group_size)
+    if scales is None:
+        _moe.grouped_gemm(c, a, b, expert_offsets, num_experts, total_rows, n, k)
+    else:
+        _moe.grouped_gemm_w4a16(c, a, b, scales, zeros, expert_offsets, num_experts,
+                                total_rows, n, k, group_size=group_size)
     return c
 
 

@@ -1,10 +1,10 @@
-"""Mixture-of-Experts: routing (``moe.h``) and the grouped W4A16 GEMM
-(extension, ``moe_w4a16.h``).
+"""Mixture-of-Experts: routing and the dense grouped GEMM (``moe.h``) and the
+grouped W4A16 GEMM (extension, ``moe_w4a16.h``).
 
-The routing wrappers keep the reference's names, argument order and return
-values (``bindings/python/kernel_set/moe.py:42-186``). The reference has no
-quantized grouped GEMM; ``grouped_gemm_w4a16`` follows the argument order of
-its dense ``grouped_gemm`` (``moe.py:189-217``) with the weight replaced by the
+The routing wrappers and ``grouped_gemm`` keep the reference's names, argument
+order and return values (``bindings/python/kernel_set/moe.py:42-217``). The
+reference has no quantized grouped GEMM; ``grouped_gemm_w4a16`` follows the
+argument order of ``grouped_gemm`` with the weight replaced by the
 ``gemm_w4a16`` format.
 """
 from __future__ import annotations
@@ -16,7 +16,7 @@ from ._lib import check, lib
 from ._tensor import TensorLike, default_stream, infer_dtype, ptr
 
 __all__ = ["gate_softmax_topk", "gate_sigmoid_group_topk", "compute_permutation", "permute",
-           "unpermute", "grouped_gemm_w4a16"]
+           "unpermute", "grouped_gemm", "grouped_gemm_w4a16"]
 
 
 def _i32(obj, *, name, allow_none=False):
@@ -100,6 +100,24 @@ def unpermute(out: TensorLike, permuted: TensorLike, sorted_token_ids: TensorLik
         dt, default_stream(stream, permuted)),
         "ks_moe_unpermute")
     return out
+
+
+def grouped_gemm(c: TensorLike, a: TensorLike, b: TensorLike, expert_offsets: TensorLike,
+                 num_experts: int, total_rows: int, n: int, k: int,
+                 dtype: Optional[int] = None, stream: TensorLike = None) -> TensorLike:
+    """For each expert ``e``: ``C[off_e:off_{e+1}] = A[off_e:off_{e+1}] @ B_e``
+    (reference ``moe.py:189-217``).
+
+    a ``[total_rows, k]``; b ``[num_experts, k, n]``; expert_offsets int32
+    ``[num_experts+1]``; c ``[total_rows, n]``, all of one dtype (f32, f16,
+    bf16, fp8 e4m3fn, fp8 e5m2)."""
+    dt = infer_dtype(a, dtype)
+    check(lib.ks_moe_grouped_gemm(
+        ptr(c, name="c"), ptr(a, name="a"), ptr(b, name="b"),
+        _i32(expert_offsets, name="expert_offsets"), int(num_experts), int(total_rows),
+        int(n), int(k), dt, default_stream(stream, a)),
+        "ks_moe_grouped_gemm")
+    return c
 
 
 def grouped_gemm_w4a16(c: TensorLike, a: TensorLike, b_packed: TensorLike,

@@ -54,6 +54,7 @@ def lib() -> ctypes.CDLL:
             "oracle_fp8_gemm": [P, P, P, P, P, I64, I64, I64, I, I, I],
             "oracle_w8a8_acc": [P, P, P, I64, I64, I64],
             "oracle_w8a8_epilogue": [P, P, P, P, P, I64, I64, I, I],
+            "oracle_grouped_gemm": [P, P, P, I, P, I64, I64, I64],
         }
         for name, args in sig.items():
             fn = getattr(L, name)
@@ -412,6 +413,37 @@ def moe_w4a16_ref(a, b_packed, scales, zeros, offsets, group_size, dtype="bf16")
             w = w4a16_dequant_weight(b_packed[e], scales[e],
                                      None if zeros is None else zeros[e], group_size, dtype)
             out[r0:r1] = a[r0:r1] @ w
+    return out
+
+
+def grouped_gemm_scalar(a, b, offsets, init=None) -> np.ndarray:
+    """Dense grouped GEMM in the reference kernel's order (moe_grouped_gemm.cu:
+    68-127, scalar C): a ``[rows, k]``, b ``[E, k, n]`` (fp32 values of the
+    storage dtype), offsets ``[E+1]``. Rows outside every expert's range keep
+    ``init`` (zeros by default). Returns fp32 before the output rounding."""
+    a = _c(a, np.float32)
+    b = _c(b, np.float32)
+    offs = _c(offsets, np.int32)
+    rows, k = a.shape
+    E, _, n = b.shape
+    out = np.zeros((rows, n), np.float32) if init is None else _c(init, np.float32).copy()
+    lib().oracle_grouped_gemm(_p(a), _p(b), _p(offs), E, _p(out), rows, n, k)
+    return out
+
+
+def grouped_gemm_ref(a, b, offsets, init=None) -> np.ndarray:
+    """The same grouped product as one fp32 matmul per expert (the closed form
+    the GEMM tolerance is stated against), for sizes the scalar loop is too
+    slow for."""
+    a = _c(a, np.float32)
+    b = _c(b, np.float32)
+    rows = a.shape[0]
+    out = np.zeros((rows, b.shape[2]), np.float32) if init is None else _c(init, np.float32).copy()
+    for e in range(b.shape[0]):
+        r0 = min(max(int(offsets[e]), 0), rows)
+        r1 = min(int(offsets[e + 1]), rows)
+        if r1 > r0:
+            out[r0:r1] = a[r0:r1] @ b[e]
     return out
 
 

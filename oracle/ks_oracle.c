@@ -244,3 +244,25 @@ void oracle_w8a8_epilogue(const int32_t* acc, const float* as, const float* bs,
       c[i * n + j] = v;
     }
 }
+
+/* moe_grouped_gemm.cu:68-127: for each expert e, rows [offs[e], offs[e+1]) of
+ * A times B_e = b + e*k*n ([k, n]), acc = fma(a, b, acc) over increasing k in
+ * fp32 (the reference's acc += as*bs, contracted to an fma). Rows outside
+ * every expert's range are not written; ranges are clamped to [0, rows].
+ * Operands already decoded to fp32; output fp32 (the caller rounds). */
+void oracle_grouped_gemm(const float* a, const float* b, const int32_t* offs, int ne,
+                         float* c, int64_t rows, int64_t n, int64_t k) {
+  for (int e = 0; e < ne; ++e) {
+    int64_t r0 = offs[e] < 0 ? 0 : offs[e];
+    int64_t r1 = offs[e + 1];
+    if (r0 > rows) r0 = rows;
+    if (r1 > rows) r1 = rows;
+    const float* be = b + (int64_t)e * k * n;
+    for (int64_t i = r0; i < r1; ++i)
+      for (int64_t j = 0; j < n; ++j) {
+        float acc = 0.0f;
+        for (int64_t kk = 0; kk < k; ++kk) acc = fmaf(a[i * k + kk], be[kk * n + j], acc);
+        c[i * n + j] = acc;
+      }
+  }
+}

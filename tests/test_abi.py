@@ -218,6 +218,23 @@ def test_moe_validation():
     assert f(P, P, P, P, None, ip, 4, 0, 16, 32, 32, DType.BF16, None) == Status.SUCCESS
 
 
+def test_dense_grouped_gemm_validation():
+    # moe_grouped_gemm.cu:140-152: NULL pointers and bad shapes are
+    # INVALID_ARGUMENT, dtypes outside f32/f16/bf16/fp8 UNSUPPORTED_DTYPE, and
+    # total_rows == 0 returns before any launch.
+    f = _lib.lib.ks_moe_grouped_gemm
+    ip = ctypes.cast(P, _lib._I32P)
+    assert f(P, P, P, None, 4, 8, 16, 32, DType.BF16, None) == Status.ERROR_INVALID_ARGUMENT
+    assert ks.last_error_string() == "null arg: expert_offsets"
+    assert f(None, P, P, ip, 4, 8, 16, 32, DType.BF16, None) == Status.ERROR_INVALID_ARGUMENT
+    for bad in ((0, 8, 16, 32), (4, -1, 16, 32), (4, 8, 0, 32), (4, 8, 16, 0)):
+        assert f(P, P, P, ip, *bad, DType.BF16, None) == Status.ERROR_INVALID_ARGUMENT
+        assert ks.last_error_string() == "ks_moe_grouped_gemm: bad shape"
+    assert f(P, P, P, ip, 4, 8, 16, 32, DType.I8, None) == Status.ERROR_UNSUPPORTED_DTYPE
+    assert f(P, P, P, ip, 4, 8, 16, 32, DType.F64, None) == Status.ERROR_UNSUPPORTED_DTYPE
+    assert f(P, P, P, ip, 4, 0, 16, 32, DType.F8E5M2, None) == Status.SUCCESS
+
+
 def test_python_wrappers_raise_kernel_set_error():
     with pytest.raises(ks.KernelSetError) as ei:
         ks.gemm.gemm_w4a16(0, P, P, P, None, 1, 8, 8, 8, dtype=DType.BF16)

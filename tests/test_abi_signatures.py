@@ -50,10 +50,11 @@ def diff(expected, actual):
 def test_table_covers_the_reference_scope():
     table = load_table()
     ref = {n for n, e in table.items() if e["ref"] != "extension"}
-    assert len(ref) == 33
+    assert len(ref) == 34
     for name in ("ks_gemm_w4a16", "ks_gemm_w8a8", "ks_gemm_fp8", "ks_gemm_fp8_blockwise",
                  "ks_quantize_fp8", "ks_quantize_fp8_group", "ks_quantize_int8",
-                 "ks_dequantize_int4", "ks_repack_int4", "ks_moe_compute_permutation"):
+                 "ks_dequantize_int4", "ks_repack_int4", "ks_moe_compute_permutation",
+                 "ks_moe_grouped_gemm"):
         assert name in ref and table[name]["ref"].startswith("include/kernel_set/")
     assert table["ks_gemm_w4a16"]["params"] == [
         "void*", "const void*", "const void*", "const void*", "const void*", "const void*",

@@ -425,3 +425,55 @@ def test_unpermute_ref_closed_forms():
     assert np.array_equal(p[::2], x) and np.array_equal(p[1::2], x)
     half = np.full((T, k), 0.5, np.float32)
     assert np.array_equal(O.unpermute_ref(p, ident, half, T, k), x)
+
+
+# ---- dense grouped GEMM (moe_grouped_gemm.cu:68-127) ----------------------
+def test_grouped_gemm_scalar_integer_case_is_exact():
+    """Small integers make every fp32 partial sum exact in any order, so the
+    scalar oracle must equal the int64 product of each expert's rows with that
+    expert's [K, N] slab (a transposed slab, a wrong expert or a dropped k
+    fails; K != N so a transpose cannot pass)."""
+    rng = np.random.default_rng(11)
+    E, K, N, rows = 5, 24, 17, 40
+    a = rng.integers(-4, 5, (rows, K))
+    b = rng.integers(-4, 5, (E, K, N))
+    offs = np.array([3, 9, 9, 22, 30, 37], np.int32)  # rows 0-2 and 37-39 unrouted
+    init = np.full((rows, N), -7.0, np.float32)
+    out = O.grouped_gemm_scalar(a.astype(np.float32), b.astype(np.float32), offs, init)
+    for e in range(E):
+        r0, r1 = offs[e], offs[e + 1]
+        np.testing.assert_array_equal(out[r0:r1], (a[r0:r1] @ b[e]).astype(np.float32))
+    np.testing.assert_array_equal(out[:3], init[:3])
+    np.testing.assert_array_equal(out[37:], init[37:])
+
+
+def test_grouped_gemm_scalar_is_sequential_fma():
+    """One expert, one output: the reference's k-ascending fp32 fma chain,
+    checked against math.fsum-free hand evaluation with np.float32 fma via
+    float64 (exact for one product plus one fp32 addend, then rounded)."""
+    rng = np.random.default_rng(12)
+    K = 50
+    a = rng.standard_normal((1, K)).astype(np.float32)
+    b = rng.standard_normal((1, K, 1)).astype(np.float32)
+    acc = np.float32(0.0)
+    for kk in range(K):  # fma(x, y, acc): x*y exact in float64, one rounding
+        acc = np.float32(np.float64(a[0, kk]) * np.float64(b[0, kk, 0]) + np.float64(acc))
+    out = O.grouped_gemm_scalar(a, b, np.array([0, 1], np.int32))
+    assert out[0, 0] == acc
+
+
+def test_grouped_gemm_ref_matches_scalar():
+    rng = np.random.default_rng(13)
+    E, K, N, rows = 3, 96, 40, 33
+    a = rng.standard_normal((rows, K)).astype(np.float32)
+    b = rng.standard_normal((E, K, N)).astype(np.float32)
+    offs = np.array([0, 10, 10, 33], np.int32)
+    s = O.grouped_gemm_scalar(a, b, offs)
+    r = O.grouped_gemm_ref(a, b, offs)
+    assert O.rel_err(s, r) < 1e-5
+    # ranges are clamped to the rows that exist: [-5, 10) is rows 0-9, [10, 4)
+    # is empty, [4, 50) is rows 4-32 (it overlaps expert 0 from row 4 on)
+    offs2 = np.array([-5, 10, 4, 50], np.int32)
+    out2 = O.grouped_gemm_scalar(a, b, offs2)
+    np.testing.assert_array_equal(out2[:4], s[:4])
+    np.testing.assert_array_equal(out2[4:], O.grouped_gemm_scalar(a[4:], b[2:], np.array([0, 29], np.int32)))
