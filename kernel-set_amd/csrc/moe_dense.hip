@@ -310,20 +310,26 @@ __device__ inline void dense_pass(typename Dt<T>::st* __restrict__ c,
   }
 }
 
+// One workgroup per (128-column tile, expert). Workgroup ids are dispatched to
+// the 8 XCDs round-robin; id L serves expert (L % 8) + 8 * (L / 8 / tiles_n),
+// so every column tile of an expert runs on one XCD and the expert's rows of A
+// come from HBM into that XCD's L2 once, not into all eight.
 template <typename T, int MB>
 __global__ void __launch_bounds__(kThreads, 2)
 dense_kernel(typename Dt<T>::st* __restrict__ c, const typename Dt<T>::st* __restrict__ a,
              const typename Dt<T>::st* __restrict__ b, const int32_t* __restrict__ offsets,
-             int64_t total_rows, int64_t n, int64_t k) {
+             int num_experts, int tiles_n, int64_t total_rows, int64_t n, int64_t k) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  const int e = blockIdx.y;
+  const int L = blockIdx.x;
+  const int e = (L & 7) + 8 * ((L >> 3) / tiles_n);
+  if (e >= num_experts) return;
   // Row range clamped to [0, total_rows]: malformed offsets cannot make the
   // kernel touch memory outside A and C.
   const int64_t r_begin = min<int64_t>(max<int64_t>(offsets[e], 0), total_rows);
   const int64_t r_end = min<int64_t>(max<int64_t>(offsets[e + 1], r_begin), total_rows);
   if (r_end <= r_begin) return;  // uniform across the workgroup
   const typename Dt<T>::st* be = b + static_cast<int64_t>(e) * k * n;
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kTileN;
+  const int64_t n0 = static_cast<int64_t>((L >> 3) % tiles_n) * kTileN;
   for (int64_t r0 = r_begin; r0 < r_end; r0 += 16 * MB)
     dense_pass<T, MB>(c, a, be, r0, r_end, n0, n, k, smem);
 }
@@ -366,9 +372,10 @@ void launch_tile(void* c, const void* a, const void* b, const int32_t* offs, int
   }();
   (void)configured;
   using S = typename Dt<T>::st;
-  const dim3 grid(static_cast<unsigned>((n + kTileN - 1) / kTileN), static_cast<unsigned>(E));
-  hipLaunchKernelGGL((dense_kernel<T, MB>), grid, dim3(kThreads), lds, st, static_cast<S*>(c),
-                     static_cast<const S*>(a), static_cast<const S*>(b), offs, rows, n, k);
+  const int tiles_n = static_cast<int>((n + kTileN - 1) / kTileN);
+  const unsigned grid = static_cast<unsigned>(tiles_n * ((E + 7) / 8) * 8);
+  hipLaunchKernelGGL((dense_kernel<T, MB>), dim3(grid), dim3(kThreads), lds, st, static_cast<S*>(c),
+                     static_cast<const S*>(a), static_cast<const S*>(b), offs, E, tiles_n, rows, n, k);
 }
 
 template <typename T>
@@ -413,7 +420,8 @@ ks_status_t ks_moe_grouped_gemm(void* c, const void* a, const void* b,
       dtype != KS_DTYPE_F8E4M3 && dtype != KS_DTYPE_F8E5M2)
     KS_FAIL(KS_ERROR_UNSUPPORTED_DTYPE, "ks_moe_grouped_gemm: unsupported dtype");
   if (total_rows == 0) return KS_SUCCESS;  // nothing routed
-  if (num_experts > 65535 || (n + ks::moed::kTileN - 1) / ks::moed::kTileN > 2147483647LL ||
+  if (num_experts > 65535 ||
+      (n + ks::moed::kTileN - 1) / ks::moed::kTileN * (num_experts + 7) > (int64_t{1} << 30) ||
       total_rows * n / ks::moed::kThreads > 2147483647LL)
     KS_FAIL(KS_ERROR_UNSUPPORTED_SHAPE, "ks_moe_grouped_gemm: shape exceeds grid limits");
   auto st = ks::to_stream(stream);

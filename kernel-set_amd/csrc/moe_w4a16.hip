@@ -64,17 +64,23 @@ moe_mfma_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
   }
 }
 
-// LDS-ring variant (gs % 64 == 0, K % 128 == 0, N % 16 == 0): grid (128-column tiles) x
-// (experts); each workgroup walks its expert's rows in 16*MB-row passes over
-// the whole K of the expert.
+// LDS-ring variant (gs % 64 == 0, K % 128 == 0, N % 16 == 0): one workgroup
+// per (128-column tile, expert) walks the expert's rows in 16*MB-row passes
+// over the whole K of the expert. Workgroup ids are dispatched to the 8 XCDs
+// round-robin; id L serves expert (L % 8) + 8 * (L / 8 / tiles_n), so every
+// column tile of an expert runs on one XCD and the expert's activation rows
+// are fetched from HBM into that XCD's L2 once, not by all eight.
 template <typename T, int MB>
 __global__ void __launch_bounds__(w4pipe::kThreads, 2)
 moe_pipe_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
                 const uint8_t* __restrict__ b, const uint16_t* __restrict__ scales,
                 const uint16_t* __restrict__ zeros, const int32_t* __restrict__ offsets,
-                int64_t total_rows, int64_t n, int64_t k, int gs) {
+                int num_experts, int tiles_n, int64_t total_rows, int64_t n, int64_t k, int gs) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  const int e = blockIdx.y;
+  const int L = blockIdx.x;
+  const int e = (L & 7) + 8 * ((L >> 3) / tiles_n);
+  const int tile = (L >> 3) % tiles_n;
+  if (e >= num_experts) return;
   const int64_t r_begin = min<int64_t>(max<int64_t>(offsets[e], 0), total_rows);
   const int64_t r_end = min<int64_t>(max<int64_t>(offsets[e + 1], r_begin), total_rows);
   if (r_end <= r_begin) return;  // uniform across the workgroup
@@ -85,7 +91,7 @@ moe_pipe_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
   p.s = scales + static_cast<int64_t>(e) * ng * n;
   p.z = zeros ? zeros + static_cast<int64_t>(e) * ng * n : nullptr;
   p.n = n; p.k = k; p.gs = gs;
-  p.n0 = static_cast<int64_t>(blockIdx.x) * w4pipe::kTileN;
+  p.n0 = static_cast<int64_t>(tile) * w4pipe::kTileN;
   const int total = static_cast<int>(k / w4pipe::kStageK);
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int li = lane % 16, q = lane / 16;
@@ -119,10 +125,10 @@ void launch_pipe(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_
     return true;
   }();
   (void)configured;
-  const dim3 grid(static_cast<unsigned>((n + w4pipe::kTileN - 1) / w4pipe::kTileN),
-                  static_cast<unsigned>(E));
-  hipLaunchKernelGGL((moe_pipe_kernel<T, MB>), grid, dim3(w4pipe::kThreads), lds, st, c, a, b, s,
-                     z, offs, rows, n, k, gs);
+  const int tiles_n = static_cast<int>((n + w4pipe::kTileN - 1) / w4pipe::kTileN);
+  const unsigned grid = static_cast<unsigned>(tiles_n * ((E + 7) / 8) * 8);
+  hipLaunchKernelGGL((moe_pipe_kernel<T, MB>), dim3(grid), dim3(w4pipe::kThreads), lds, st, c, a,
+                     b, s, z, offs, E, tiles_n, rows, n, k, gs);
 }
 
 // Any-shape fallback: one thread per (row, column); the expert is found by a
@@ -224,7 +230,8 @@ ks_status_t ks_moe_grouped_gemm_w4a16(void* c, const void* a, const void* b_pack
     KS_FAIL(KS_ERROR_UNSUPPORTED_SHAPE, "ks_moe_grouped_gemm_w4a16: group_size must divide K");
   if (dtype != KS_DTYPE_F16 && dtype != KS_DTYPE_BF16)
     KS_FAIL(KS_ERROR_UNSUPPORTED_DTYPE, "ks_moe_grouped_gemm_w4a16: dtype must be f16 or bf16");
-  if (num_experts > 65535 || k > 2147483647LL || n > (int64_t{1} << 36))
+  if (num_experts > 65535 || k > 2147483647LL || n > (int64_t{1} << 36) ||
+      (n + 63) / 64 * (num_experts + 7) > (int64_t{1} << 30))
     KS_FAIL(KS_ERROR_UNSUPPORTED_SHAPE, "ks_moe_grouped_gemm_w4a16: shape exceeds grid limits");
   if (total_rows == 0) return KS_SUCCESS;  // nothing routed
   auto st = ks::to_stream(stream);
