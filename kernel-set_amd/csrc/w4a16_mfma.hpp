@@ -91,6 +91,22 @@ __device__ inline u32x4v codes_to_frag(uint32_t t) {
   return u32x4v{(t & m) | mg, ((t >> 4) & m) | mg, ((t >> 8) & m) | mg, ((t >> 12) & m) | mg};
 }
 
+// One column's 8 codes (packed rows in the 4 bytes of t) -> B fragment in
+// natural k order: dword r = codes (2r, 2r+1), the low and high nibble of byte
+// r, so the A fragment is 8 consecutive activations as loaded. v_perm puts
+// byte r of t in byte 0 and byte r of t >> 4 in byte 2 (zeros elsewhere), one
+// v_and_or_b32 keeps the two nibbles and adds the 128 base. `mask` must be the
+// wave-uniform 0x000f000f and `base` the magic in a VGPR (VOP3 takes no
+// literal on gfx9, and one SGPR per instruction), or the and-or splits in two.
+template <typename T>
+__device__ inline u32x4v codes_to_frag_nat(uint32_t t, uint32_t mask, uint32_t base) {
+  const uint32_t t4 = t >> 4;
+  return u32x4v{(__builtin_amdgcn_perm(t4, t, 0x0c040c00u) & mask) | base,
+                (__builtin_amdgcn_perm(t4, t, 0x0c050c01u) & mask) | base,
+                (__builtin_amdgcn_perm(t4, t, 0x0c060c02u) & mask) | base,
+                (__builtin_amdgcn_perm(t4, t, 0x0c070c03u) & mask) | base};
+}
+
 // 8 consecutive activations (16 B) -> A fragment in the (0,4),(1,5),(2,6),(3,7) order.
 __device__ inline u32x4v act_frag(uint4 d) {
   return u32x4v{__builtin_amdgcn_perm(d.z, d.x, 0x05040100u),

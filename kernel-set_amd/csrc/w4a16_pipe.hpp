@@ -18,9 +18,10 @@
 //                                  (slots 0, 1) and last 64 k (slots 2, 3)
 // B fragments are read already transposed with ds_read_b64_tr_b8: lane li of
 // 16-lane group q receives column li's bytes of packed rows 32h+8q..+7, i.e.
-// codes k = 64h+16q..+15. Each dword (8 codes) becomes an MFMA B fragment with
-// one and-or per pair: 0x4300|q is bf16 128+q (f16 0x5800|q = 128+q/8), pairs
-// ordered (0,4),(1,5),(2,6),(3,7); the activation fragment uses that order.
+// codes k = 64h+16q..+15. Each dword (8 codes) becomes an MFMA B fragment in
+// natural k order with one v_perm and one v_and_or per pair: 0x4300|q is bf16
+// 128+q (f16 0x5800|q = 128+q/8). The activation fragment is then the 16 bytes
+// read from LDS as they are, shared unchanged by the four waves.
 // Per quantization group the MFMAs accumulate P = A*(128+q) and S = A*1, then
 //   O += s * (P - (128 + z) * S)   (f16: the code axis is scaled by 1/8),
 // which is sum_k a*(q - z)*s over the group in fp32.
@@ -156,6 +157,9 @@ __device__ inline void pipe_tile(const PipeArgs& p, int64_t r0, int64_t r_end, i
 
   const u32x4v ones = {w4mma::mfma_traits<T>::one2, w4mma::mfma_traits<T>::one2,
                        w4mma::mfma_traits<T>::one2, w4mma::mfma_traits<T>::one2};
+  uint32_t code_base = w4mma::mfma_traits<T>::magic;
+  asm volatile("" : "+v"(code_base));  // kept in a VGPR (see codes_to_frag_nat)
+  const uint32_t code_mask = __builtin_amdgcn_readfirstlane(0x000f000fu);
   constexpr float unit = w4mma::code_scale<T>::unit;
   constexpr float inv_unit = 1.0f / unit;
   const bool has_z = p.z != nullptr;
@@ -224,10 +228,10 @@ __device__ inline void pipe_tile(const PipeArgs& p, int64_t r0, int64_t r_end, i
       const i32x2 d1 = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
           reinterpret_cast<lds_i32x2*>(reinterpret_cast<uintptr_t>(wl + tr_pc1)));
       u32x4v bfr[2][2];
-      bfr[0][0] = w4mma::codes_to_frag<T>(static_cast<uint32_t>(d0[0]));
-      bfr[0][1] = w4mma::codes_to_frag<T>(static_cast<uint32_t>(d0[1]));
-      bfr[1][0] = w4mma::codes_to_frag<T>(static_cast<uint32_t>(d1[0]));
-      bfr[1][1] = w4mma::codes_to_frag<T>(static_cast<uint32_t>(d1[1]));
+      bfr[0][0] = w4mma::codes_to_frag_nat<T>(static_cast<uint32_t>(d0[0]), code_mask, code_base);
+      bfr[0][1] = w4mma::codes_to_frag_nat<T>(static_cast<uint32_t>(d0[1]), code_mask, code_base);
+      bfr[1][0] = w4mma::codes_to_frag_nat<T>(static_cast<uint32_t>(d1[0]), code_mask, code_base);
+      bfr[1][1] = w4mma::codes_to_frag_nat<T>(static_cast<uint32_t>(d1[1]), code_mask, code_base);
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
         const int row = 16 * mb + li;
@@ -235,7 +239,7 @@ __device__ inline void pipe_tile(const PipeArgs& p, int64_t r0, int64_t r_end, i
         for (int sub = 0; sub < 2; ++sub) {
           const int pc = (8 * h + 2 * q + sub) ^ li;  // row & 15 == li
           const uint4 v = *reinterpret_cast<const uint4*>(al + row * 256 + pc * 16);
-          const u32x4v af = w4mma::act_frag(v);
+          const u32x4v af = {v.x, v.y, v.z, v.w};
           P[mb][0] = w4mma::mfma_traits<T>::mma(af, bfr[0][sub], P[mb][0]);
           P[mb][1] = w4mma::mfma_traits<T>::mma(af, bfr[1][sub], P[mb][1]);
           S[mb] = w4mma::mfma_traits<T>::mma(af, ones, S[mb]);
