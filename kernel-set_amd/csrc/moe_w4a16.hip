@@ -70,7 +70,7 @@ moe_mfma_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
 // round-robin; id L serves expert (L % 8) + 8 * (L / 8 / tiles_n), so every
 // column tile of an expert runs on one XCD and the expert's activation rows
 // are fetched from HBM into that XCD's L2 once, not by all eight.
-template <typename T, int MB>
+template <typename T, int MB, bool OG>
 __global__ void __launch_bounds__(w4pipe::kThreads, 2)
 moe_pipe_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
                 const uint8_t* __restrict__ b, const uint16_t* __restrict__ scales,
@@ -97,7 +97,7 @@ moe_pipe_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
   const int li = lane % 16, q = lane / 16;
   for (int64_t r0 = r_begin; r0 < r_end; r0 += 16 * MB) {
     w4mma::f32x4 O[MB][2];
-    w4pipe::pipe_tile<T, MB>(p, r0, r_end, 0, total, smem, O);
+    w4pipe::pipe_tile<T, MB, OG>(p, r0, r_end, 0, total, smem, O);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int64_t col = p.n0 + 32 * wave + 16 * j + li;
@@ -113,22 +113,33 @@ moe_pipe_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
   }
 }
 
-template <typename T, int MB>
-void launch_pipe(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_t* s,
-                 const uint16_t* z, const int32_t* offs, int E, int64_t rows, int64_t n,
-                 int64_t k, int gs, hipStream_t st) {
+template <typename T, int MB, bool OG>
+void launch_pipe_og(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_t* s,
+                    const uint16_t* z, const int32_t* offs, int E, int64_t rows, int64_t n,
+                    int64_t k, int gs, hipStream_t st) {
   constexpr int lds = w4pipe::Ring<MB>::kBytes;
   // opt in to the LDS size once per process (thread-safe static initialization)
   static const bool configured = [] {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_pipe_kernel<T, MB>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_pipe_kernel<T, MB, OG>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     return true;
   }();
   (void)configured;
   const int tiles_n = static_cast<int>((n + w4pipe::kTileN - 1) / w4pipe::kTileN);
   const unsigned grid = static_cast<unsigned>(tiles_n * ((E + 7) / 8) * 8);
-  hipLaunchKernelGGL((moe_pipe_kernel<T, MB>), dim3(grid), dim3(w4pipe::kThreads), lds, st, c, a,
-                     b, s, z, offs, E, tiles_n, rows, n, k, gs);
+  hipLaunchKernelGGL((moe_pipe_kernel<T, MB, OG>), dim3(grid), dim3(w4pipe::kThreads), lds, st, c,
+                     a, b, s, z, offs, E, tiles_n, rows, n, k, gs);
+}
+
+// gs == 128: the one-group-per-stage variant of the ring tile.
+template <typename T, int MB>
+void launch_pipe(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_t* s,
+                 const uint16_t* z, const int32_t* offs, int E, int64_t rows, int64_t n,
+                 int64_t k, int gs, hipStream_t st) {
+  if (gs == w4pipe::kStageK)
+    launch_pipe_og<T, MB, true>(c, a, b, s, z, offs, E, rows, n, k, gs, st);
+  else
+    launch_pipe_og<T, MB, false>(c, a, b, s, z, offs, E, rows, n, k, gs, st);
 }
 
 // Any-shape fallback: one thread per (row, column); the expert is found by a

@@ -354,7 +354,7 @@ ks_status_t run_mfma(uint16_t* c, const uint16_t* a, const uint8_t* b, const uin
 
 // Batched path on the LDS-ring tile: one launch covers rows [row0, row1)
 // (<= 16*MB rows) for every 128-column tile and K split.
-template <typename T, int MB>
+template <typename T, int MB, bool OG>
 __global__ void __launch_bounds__(w4pipe::kThreads, 2)
 pipe_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
             const uint8_t* __restrict__ b, const uint16_t* __restrict__ scales,
@@ -372,7 +372,7 @@ pipe_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
   const int st0 = split * stages_per_split;
   const int st1 = min(st0 + stages_per_split, total);
   w4mma::f32x4 O[MB][2];
-  w4pipe::pipe_tile<T, MB>(p, row0, row1, st0, st1, smem, O);
+  w4pipe::pipe_tile<T, MB, OG>(p, row0, row1, st0, st1, smem, O);
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int li = lane % 16, q = lane / 16;
   const int64_t rows = row1 - row0;
@@ -395,21 +395,33 @@ pipe_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
   }
 }
 
-template <typename T, int MB>
-void launch_pipe(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_t* s,
-                 const uint16_t* z, const uint16_t* bias, int64_t r0, int64_t r1, int64_t n,
-                 int64_t k, int gs, int tiles, int splits, int sps, float* ws, hipStream_t st) {
+template <typename T, int MB, bool OG>
+void launch_pipe_og(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_t* s,
+                    const uint16_t* z, const uint16_t* bias, int64_t r0, int64_t r1, int64_t n,
+                    int64_t k, int gs, int tiles, int splits, int sps, float* ws, hipStream_t st) {
   constexpr int lds = w4pipe::Ring<MB>::kBytes;
   // opt in to the LDS size once per process (thread-safe static initialization)
   static const bool configured = [] {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&pipe_kernel<T, MB>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&pipe_kernel<T, MB, OG>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     return true;
   }();
   (void)configured;
-  hipLaunchKernelGGL((pipe_kernel<T, MB>), dim3(static_cast<unsigned>(tiles * splits)),
+  hipLaunchKernelGGL((pipe_kernel<T, MB, OG>), dim3(static_cast<unsigned>(tiles * splits)),
                      dim3(w4pipe::kThreads), lds, st, c, a, b, s, z, bias, r0, r1, n, k, gs,
                      splits, sps, ws);
+}
+
+// gs == 128 (one quantization group per 128-k stage) takes the variant whose
+// stage-opening MFMAs start from zero instead of clearing the accumulators.
+template <typename T, int MB>
+void launch_pipe(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_t* s,
+                 const uint16_t* z, const uint16_t* bias, int64_t r0, int64_t r1, int64_t n,
+                 int64_t k, int gs, int tiles, int splits, int sps, float* ws, hipStream_t st) {
+  if (gs == w4pipe::kStageK)
+    launch_pipe_og<T, MB, true>(c, a, b, s, z, bias, r0, r1, n, k, gs, tiles, splits, sps, ws, st);
+  else
+    launch_pipe_og<T, MB, false>(c, a, b, s, z, bias, r0, r1, n, k, gs, tiles, splits, sps, ws, st);
 }
 
 template <typename T>

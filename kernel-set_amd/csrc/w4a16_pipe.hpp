@@ -79,7 +79,9 @@ struct PipeArgs {
 // n0 + 32*wave + 16*j + li. Requires K % 128 == 0, gs % 64 == 0, N % 16 == 0,
 // 16-byte aligned a / b, 4-byte aligned scales / zeros, and st0 on a
 // quantization-group boundary. All threads of the workgroup must call it.
-template <typename T, int MB>
+// OG (one group per stage, gs == 128): each stage's first MFMAs start from a
+// zero accumulator, so the promotion clears no P / S registers.
+template <typename T, int MB, bool OG = false>
 __device__ inline void pipe_tile(const PipeArgs& p, int64_t r0, int64_t r_end, int st0, int st1,
                                  uint8_t* smem, f32x4 (&O)[MB][2]) {
   using R = Ring<MB>;
@@ -184,7 +186,8 @@ __device__ inline void pipe_tile(const PipeArgs& p, int64_t r0, int64_t r_end, i
   }
 
   // Promotion with the scale/zero slot pair `half` (0: first 64 k, 1: last);
-  // leaves P and S cleared for the next group.
+  // leaves P and S cleared for the next group (OG: the next stage's first
+  // MFMAs overwrite them instead).
   auto promote = [&](const uint8_t* szl, int half) {
     const uint16_t* sl = reinterpret_cast<const uint16_t*>(szl + 512 * half);
     const uint16_t* zl = reinterpret_cast<const uint16_t*>(szl + 512 * half + 256);
@@ -200,12 +203,15 @@ __device__ inline void pipe_tile(const PipeArgs& p, int64_t r0, int64_t r_end, i
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           O[mb][j][r] = fmaf(se, fmaf(-cz, S[mb][r], P[mb][j][r]), O[mb][j][r]);
-          P[mb][j][r] = 0.f;
+          if constexpr (!OG) P[mb][j][r] = 0.f;
         }
     }
+    if constexpr (!OG) {
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) S[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int mb = 0; mb < MB; ++mb) S[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
   };
+  const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
 
   int grp_pos = 0;  // stage index within its group (gs >= 128); st0 is group-aligned
   uint32_t slot_i = 0;
@@ -240,14 +246,17 @@ __device__ inline void pipe_tile(const PipeArgs& p, int64_t r0, int64_t r_end, i
           const int pc = (8 * h + 2 * q + sub) ^ li;  // row & 15 == li
           const uint4 v = *reinterpret_cast<const uint4*>(al + row * 256 + pc * 16);
           const u32x4v af = {v.x, v.y, v.z, v.w};
-          P[mb][0] = w4mma::mfma_traits<T>::mma(af, bfr[0][sub], P[mb][0]);
-          P[mb][1] = w4mma::mfma_traits<T>::mma(af, bfr[1][sub], P[mb][1]);
-          S[mb] = w4mma::mfma_traits<T>::mma(af, ones, S[mb]);
+          const bool fresh = OG && h == 0 && sub == 0;  // compile-time
+          P[mb][0] = w4mma::mfma_traits<T>::mma(af, bfr[0][sub], fresh ? zero4 : P[mb][0]);
+          P[mb][1] = w4mma::mfma_traits<T>::mma(af, bfr[1][sub], fresh ? zero4 : P[mb][1]);
+          S[mb] = w4mma::mfma_traits<T>::mma(af, ones, fresh ? zero4 : S[mb]);
         }
       }
-      if (half_groups) promote(szl, h);
+      if (!OG && half_groups) promote(szl, h);
     }
-    if (!half_groups) {
+    if constexpr (OG) {
+      promote(szl, 0);
+    } else if (!half_groups) {
       if (++grp_pos == sps || i == nst - 1) {
         grp_pos = 0;
         promote(szl, 0);
