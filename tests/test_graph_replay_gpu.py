@@ -85,7 +85,37 @@ def _quant_group(m, k, g):
     return fn, (q, s)
 
 
+def _moe_offsets(counts):
+    import numpy as np
+    return torch.tensor(np.concatenate([[0], np.cumsum(counts)]).astype("int32"), device=DEV)
+
+
+def _moe_dense(dtype, g, counts=(5, 0, 40, 17, 64, 3, 0, 30), k=512, n=384):
+    rows = sum(counts)
+    E = len(counts)
+    a = torch.randn(rows, k, device=DEV, generator=g).to(dtype)
+    b = (torch.randn(E, k, n, device=DEV, generator=g) * 0.05).to(dtype)
+    offs = _moe_offsets(counts)
+    c = torch.empty(rows, n, device=DEV, dtype=dtype)  # every row is routed
+    return lambda: ks.moe.grouped_gemm(c, a, b, offs, E, rows, n, k), c
+
+
+def _moe_w4(g, counts=(5, 0, 40, 17, 64, 3, 0, 30), k=512, n=384, gs=128):
+    rows = sum(counts)
+    E = len(counts)
+    a = torch.randn(rows, k, device=DEV, generator=g).to(torch.bfloat16)
+    b = torch.randint(0, 256, (E, k // 2, n), device=DEV, dtype=torch.uint8, generator=g)
+    s = (torch.rand(E, k // gs, n, device=DEV, generator=g) * 0.018 + 0.002).to(torch.bfloat16)
+    offs = _moe_offsets(counts)
+    c = torch.empty(rows, n, device=DEV, dtype=torch.bfloat16)
+    return lambda: ks.moe.grouped_gemm_w4a16(c, a, b, s, None, offs, E, rows, n, k, gs), c
+
+
 CASES = {
+    "moe_dense_bf16": lambda g: _moe_dense(torch.bfloat16, g),
+    "moe_dense_fp8": lambda g: _moe_dense(torch.float8_e4m3fn, g),
+    "moe_dense_f32": lambda g: _moe_dense(torch.float32, g),
+    "moe_w4a16_ring": lambda g: _moe_w4(g),
     "w4a16_decode_M1": lambda g: _w4(1, 4096, 4096, g),
     "w4a16_decode_M8": lambda g: _w4(8, 4096, 4096, g),
     "w4a16_ring_M16": lambda g: _w4(16, 4096, 4096, g),
