@@ -5,12 +5,14 @@
 // of cklxx/kernel-set: CSR expert_offsets, rows of A/C grouped by expert) with
 // the weight operand in the ks_gemm_w4a16 format (gemm_w4a16.cu:1-17).
 //
-// No schedule buffer, no allocation, no stream synchronization: the grid is
-// (64-column tiles) x (experts), every workgroup reads its expert's row range
-// straight from expert_offsets and walks it in 16*MB-row passes with the
-// shared MFMA tile routine. All K of the expert is handled inside the
-// workgroup (4 waves split it), so each expert weight byte is read from HBM
-// once per pass; decode-sized experts (<= 16*MB rows) need a single pass.
+// No schedule buffer, no allocation, no stream synchronization: one workgroup
+// per (column tile, expert) reads its expert's row range straight from
+// expert_offsets and walks it in 16*MB-row passes, all of K per workgroup, so
+// each expert weight byte is read from HBM once per pass; decode-sized experts
+// (<= 16*MB rows) need a single pass. The main form is the LDS-ring tile of
+// w4a16_pipe.hpp (128-column tiles, moe_pipe_kernel); shapes it does not take
+// run the 64-column register tile (moe_mfma_kernel, 4 waves split K) or the
+// per-element fallback.
 // Row ranges are clamped to [0, total_rows], so malformed offsets cannot make
 // the kernel touch memory outside A and C.
 #include <algorithm>
