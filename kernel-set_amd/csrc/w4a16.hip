@@ -630,7 +630,7 @@ template <typename T>
 bool run_dec(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_t* s,
              const uint16_t* z, const uint16_t* bias, int64_t m, int64_t n, int64_t k, int gs,
              hipStream_t st, ks_status_t* r) {
-  if (n % 16 != 0 || k % 8 != 0 || n > (int64_t{1} << 30) || k > (int64_t{1} << 30) ||
+  if (n % 16 != 0 || k % 8 != 0 || n > (int64_t{1} << 26) || k > (int64_t{1} << 30) ||
       !aligned(a, 16) ||
       !aligned(b, 16) || !aligned(s, 16) || !aligned(z, 16))
     return false;

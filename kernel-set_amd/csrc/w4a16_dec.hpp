@@ -126,15 +126,21 @@ dec_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
 #pragma unroll
       for (int i = 0; i < RPT / 4; ++i) ch.a[mb][i] = src[i];
     }
+    // Weight addresses: a wave-uniform row base (a wave's 4*RPT rows are all
+    // in range or all out, since K/2 is a multiple of 4*RPT) plus a 32-bit
+    // lane offset, one add per load instead of a 64-bit multiply-add.
+    const uint8_t* bw = b + static_cast<int64_t>(wrow0 < kph ? wrow0 : 0) * n;
+    const uint32_t loff = static_cast<uint32_t>(g * RPT * n + ccol0);
+#pragma unroll
+    for (int i = 0; i < RPT; ++i)
+      ch.w[i] = load_stream16(bw + (loff + static_cast<uint32_t>(i * n)));
+    // The group's scales / zeros are needed only by the promotion: issued last.
     const int grp = min((2 * wrow0) / gs, ng - 1);
     const int64_t gi = static_cast<int64_t>(grp) * n + ccol0;
     ch.s[0] = *reinterpret_cast<const uint4*>(scales + gi);
     ch.s[1] = *reinterpret_cast<const uint4*>(scales + gi + 8);
     ch.z[0] = *reinterpret_cast<const uint4*>(zsrc + gi);
     ch.z[1] = *reinterpret_cast<const uint4*>(zsrc + gi + 8);
-#pragma unroll
-    for (int i = 0; i < RPT; ++i)
-      ch.w[i] = load_stream16(b + static_cast<int64_t>(crow0 + i) * n + ccol0);
   };
 
   // Per-lane perm selectors placing a_even / a_odd into the slots of column cdw.
