@@ -78,6 +78,22 @@ struct dq_traits<f16_t> {
   }
 };
 
+// Dequantizes the 8 codes of one packed dword (byte r = rows r: low nibble k
+// even, high nibble k odd) into 4 packed pairs o[r] = (w(k even), w(k odd)),
+// w = fma(q, s, -zs). The two nibble planes are split with one mask each and
+// every byte then converts with one v_cvt_f32_ubyteN (no per-code extract).
+template <typename T>
+__device__ inline void dequant_dword(uint32_t d, float s, float mzs, uint32_t* o) {
+  uint32_t lo = d & 0x0f0f0f0fu, hi = (d >> 4) & 0x0f0f0f0fu;
+  // opaque to the compiler, which would otherwise fold each byte back into a
+  // per-code bit-field extract
+  asm volatile("" : "+v"(lo), "+v"(hi));
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    o[r] = dq_traits<T>::pack(fmaf(static_cast<float>((lo >> (8 * r)) & 0xffu), s, mzs),
+                              fmaf(static_cast<float>((hi >> (8 * r)) & 0xffu), s, mzs));
+}
+
 template <int N>
 __device__ inline void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
@@ -175,13 +191,8 @@ dq_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
     const i32x2 d = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
         reinterpret_cast<lds_i32x2*>(reinterpret_cast<uintptr_t>(wslot + dq_src)));
     uint32_t o[8];
-#pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      const uint32_t byte = (static_cast<uint32_t>(d[r / 4]) >> (8 * (r % 4))) & 0xffu;
-      const float lo = fmaf(static_cast<float>(byte & 15u), s, -zs);
-      const float hi = fmaf(static_cast<float>(byte >> 4), s, -zs);
-      o[r] = dq_traits<T>::pack(lo, hi);
-    }
+    dequant_dword<T>(static_cast<uint32_t>(d[0]), s, -zs, o);
+    dequant_dword<T>(static_cast<uint32_t>(d[1]), s, -zs, o + 4);
     uint8_t* dst = wd_buf + dq_n * 128;
     *reinterpret_cast<uint4*>(dst + ((2 * dq_rg) ^ (dq_n & 7)) * 16) = make_uint4(o[0], o[1], o[2], o[3]);
     *reinterpret_cast<uint4*>(dst + ((2 * dq_rg + 1) ^ (dq_n & 7)) * 16) = make_uint4(o[4], o[5], o[6], o[7]);

@@ -143,13 +143,8 @@ dqs_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
       const float z = has_z ? elem<T>::to_f32(zr[h]) : 0.f;
       const float zs = s * z;  // exact: at most 2 x 11 significant bits
       uint32_t o[8];
-#pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        const uint32_t byte = (static_cast<uint32_t>(d[h][r / 4]) >> (8 * (r % 4))) & 0xffu;
-        const float lo = fmaf(static_cast<float>(byte & 15u), s, -zs);
-        const float hi = fmaf(static_cast<float>(byte >> 4), s, -zs);
-        o[r] = dq_traits<T>::pack(lo, hi);
-      }
+      w4dq::dequant_dword<T>(static_cast<uint32_t>(d[h][0]), s, -zs, o);
+      w4dq::dequant_dword<T>(static_cast<uint32_t>(d[h][1]), s, -zs, o + 4);
       uint8_t* dst = wd_buf + dn * 128;
       *reinterpret_cast<uint4*>(dst + ((2 * p) ^ (dn & 7)) * 16) = make_uint4(o[0], o[1], o[2], o[3]);
       *reinterpret_cast<uint4*>(dst + ((2 * p + 1) ^ (dn & 7)) * 16) = make_uint4(o[4], o[5], o[6], o[7]);
