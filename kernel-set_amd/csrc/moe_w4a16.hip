@@ -199,6 +199,7 @@ void run(void* c_, const void* a_, const void* b_, const void* s_, const void* z
   }
   const int64_t avg = (rows + E - 1) / E;
   const bool pipe = (gs % 64 == 0) && (k % w4pipe::kStageK == 0) && (n % 16 == 0) && aligned(a, 16) &&
+                    n < (int64_t{1} << 26) && rows * k < (int64_t{1} << 31) &&  // 32-bit copy offsets
                     aligned(b, 16) && aligned(s, 4) && aligned(z, 4);
   if (pipe) {
     // Pass height from the average rows per expert: an expert taller than a

@@ -662,7 +662,8 @@ ks_status_t run(void* c_, const void* a_, const void* b_, const void* s_, const 
                     aligned(s, 8) && aligned(z, 8) && aligned(b, 4);
   const bool pipe = m > kMaxGemvM && (gs % 64 == 0) && (k % w4pipe::kStageK == 0) && (n % 16 == 0) &&
                     aligned(a, 16) && aligned(b, 16) && aligned(s, 4) && aligned(z, 4) &&
-                    k * n < (int64_t{1} << 40);
+                    k * n < (int64_t{1} << 40) && n < (int64_t{1} << 26) &&
+                    m * k < (int64_t{1} << 31);  // the ring tile's 32-bit copy offsets
   // M <= 8: the MFMA decode kernel (measured on MI355X at K=4096, N=14336:
   // M=8 14.7 us against 33.3 us for the dot2 kernel; at M=16, four
   // block-diagonal row blocks measured 25 us against 18.8 us for the LDS-ring

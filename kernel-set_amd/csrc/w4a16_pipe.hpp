@@ -78,7 +78,9 @@ struct PipeArgs {
 // (rows >= r_end read row r_end - 1 and must not be stored) and columns
 // n0 + 32*wave + 16*j + li. Requires K % 128 == 0, gs % 64 == 0, N % 16 == 0,
 // 16-byte aligned a / b, 4-byte aligned scales / zeros, and st0 on a
-// quantization-group boundary. All threads of the workgroup must call it.
+// quantization-group boundary, and 32-bit byte offsets: 64 * N and
+// rows(A) * K * 2 below 2^32 (checked on the host). All threads of the
+// workgroup must call it.
 // OG (one group per stage, gs == 128): each stage's first MFMAs start from a
 // zero accumulator, so the promotion clears no P / S registers.
 template <typename T, int MB, bool OG = false>
@@ -100,32 +102,36 @@ __device__ inline void pipe_tile(const PipeArgs& p, int64_t r0, int64_t r_end, i
   const int nst = st1 - st0;
   if (nst <= 0) return;
 
-  // ---- ring producer: per-lane sources, advanced by one stage per issue() ----
+  // ---- ring producer: wave-uniform bases (advanced one stage per issue(),
+  // scalar adds) plus fixed 32-bit per-lane byte offsets ----
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   // W: wave instruction i fills packed rows 8*(2*wave+i)..+7 (1 KB).
-  const uint8_t* w_cur[2];
+  const uint8_t* w_base = p.b + static_cast<int64_t>(st0) * kStageRows * n;
+  uint32_t w_off[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int row = 8 * (2 * wave + i) + lane / 8;
     const int c = (lane % 8) ^ (row & 7);
     const int64_t col = min<int64_t>(p.n0 / 16 + c, last_chunk) * 16;
-    w_cur[i] = p.b + (static_cast<int64_t>(st0) * kStageRows + row) * n + col;
+    w_off[i] = static_cast<uint32_t>(row * n + col);
   }
   // A: wave instruction i fills rows 4*(wave*MB+i)..+3 (256 B per row).
-  const uint16_t* a_cur[R::kALoads];
+  const uint8_t* a_base = reinterpret_cast<const uint8_t*>(p.a) + static_cast<int64_t>(st0) * kStageK * 2;
+  uint32_t a_off[R::kALoads];
 #pragma unroll
   for (int i = 0; i < R::kALoads; ++i) {
     const int row = 4 * (wave * MB + i) + lane / 16;
     const int c = (lane % 16) ^ (row & 15);
     const int64_t gr = min<int64_t>(r0 + row, r_end - 1);
-    a_cur[i] = p.a + gr * k + static_cast<int64_t>(st0) * kStageK + 8 * c;
+    a_off[i] = static_cast<uint32_t>((gr * k + 8 * c) * 2);
   }
   // SZ: waves 0/1 take scales/zeros of the stage's first 64 k, waves 2/3 of
   // its last 64 k (the same group unless gs == 64); scales stand in for
   // absent zeros so every wave issues the same loads.
-  const uint16_t* sz_src = ((wave & 1) && p.z) ? p.z : p.s;
-  const int64_t sz_col = min<int64_t>(p.n0 + 2 * lane, n - 2);
-  const int64_t k_first = static_cast<int64_t>(st0) * kStageK + (wave >= 2 ? 64 : 0);
-  const uint16_t* sz_cur = sz_src + (k_first / p.gs) * n + sz_col;
+  const uint16_t* sz_src = ((wave_u & 1) && p.z) ? p.z : p.s;
+  const uint32_t sz_off = static_cast<uint32_t>(min<int64_t>(p.n0 + 2 * lane, n - 2) * 2);
+  const int64_t k_first = static_cast<int64_t>(st0) * kStageK + (wave_u >= 2 ? 64 : 0);
+  const uint16_t* sz_base = sz_src + (k_first / p.gs) * n;
   const int spg64 = p.gs / 64;  // 64-k halves per group
   // halves left before this wave's group index changes
   int sz_left = spg64 - static_cast<int>((k_first / 64) % spg64);
@@ -135,23 +141,20 @@ __device__ inline void pipe_tile(const PipeArgs& p, int64_t r0, int64_t r_end, i
   auto issue = [&]() {
     uint8_t* slot = smem + is_slot * R::kSlot;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      dma_to_lds<16>(w_cur[i], slot + 1024 * (2 * wave + i));
-      w_cur[i] += w_step;
-    }
+    for (int i = 0; i < 2; ++i) dma_to_lds_off<16>(w_base, w_off[i], slot + 1024 * (2 * wave_u + i));
+    w_base += w_step;
 #pragma unroll
-    for (int i = 0; i < R::kALoads; ++i) {
-      dma_to_lds<16>(a_cur[i], slot + kWBytes + 1024 * (wave * MB + i));
-      a_cur[i] += kStageK;
-    }
-    dma_to_lds<4>(sz_cur, slot + kWBytes + R::kABytes + 256 * wave);
+    for (int i = 0; i < R::kALoads; ++i)
+      dma_to_lds_off<16>(a_base, a_off[i], slot + kWBytes + 1024 * (wave_u * MB + i));
+    a_base += kStageK * 2;
+    dma_to_lds_off<4>(sz_base, sz_off, slot + kWBytes + R::kABytes + 256 * wave_u);
     sz_left -= 2;  // a stage is two 64-k halves
     if (sz_left <= 0) {
       sz_left += spg64;
-      sz_cur += n;
+      sz_base += n;
       if (sz_left <= 0) {  // gs == 64: both halves moved on
         sz_left += spg64;
-        sz_cur += n;
+        sz_base += n;
       }
     }
     is_slot = (is_slot + 1 == D) ? 0 : is_slot + 1;
