@@ -432,8 +432,10 @@ gemm8_fast_kernel(Args p) {
   // at the head of the first row blocks, after the step's B-fragment reads:
   // issuing all of them at the step start stalled every wave on the copy
   // queue before its first MFMA (fp8 blockwise M=2048 N=K=7168: 141-146 ->
-  // 124-127 us).
-  constexpr int kDmaPer = 5;
+  // 124-127 us). The kinds without promotion spread them thinner (three per
+  // row block: plain fp8 at that shape 105.5 -> 101.0 us, W8A8 4096^3
+  // 69.2 -> 68.6 us; the blockwise kind is slower at three).
+  constexpr int kDmaPer = kFp8 ? 5 : 3;
   static_assert(kDmaPer * kRB >= kL, "every copy gets a row block");
 
   f32x4 acc_o[kRB][4];
