@@ -1,10 +1,14 @@
 // kernel-set (MI355X build) -- W4A16 batched tile with an LDS load ring, shared
 // by the dense GEMM (ks_gemm_w4a16, M > 8) and the MoE grouped GEMM.
 //
-// Why a ring: at these sizes the kernel is HBM-bound (M <= 64) and a workgroup
-// has only a few MFMAs per k step, so a one-step prefetch leaves the HBM
-// latency (~2 us under load) exposed every step. Here every operand moves
-// global -> LDS directly (global_load_lds, no VGPRs held), D stages deep.
+// Every operand moves global -> LDS directly (global_load_lds, no VGPRs
+// held) through a ring of D stages. Measured on MI355X (graph replay, cold,
+// K = 4096, N = 14336), two stages beat deeper rings at every pass height
+// (M = 16 / 32 / 64: 12.5 / 15.8 / 23.5 us against 15.0 / 16.9 / 24.2 us with
+// 6 / 4 / 3 stages; MoE config 5 gate_up 41 -> 37 us): a small ring lets more
+// workgroups share a CU (48-row MoE passes: three instead of two, so the
+// 768 (tile, expert) workgroups run in one round), and the other workgroups
+// on the CU hide the copy latency that one stage of prefetch leaves exposed.
 // Measured on MI355X the tile is instruction-issue bound before it is HBM
 // bound, so a stage is 128 k deep and all per-stage bookkeeping is
 // incremental (no division, no 64-bit multiply in the loop).
@@ -50,7 +54,7 @@ template <int MB>
 struct Ring {
   static constexpr int kABytes = 16 * MB * 256;
   static constexpr int kSlot = kWBytes + kABytes + kSZBytes;
-  static constexpr int kDepth = MB >= 3 ? 3 : (MB == 2 ? 4 : 6);  // <= ~75 KB: two workgroups per CU
+  static constexpr int kDepth = 2;  // 26 / 34 / 42 / 50 KB for MB = 1..4
   static constexpr int kBytes = kSlot * kDepth;
   static constexpr int kALoads = MB;  // 16-byte A loads per thread per stage
   // global_load_lds instructions per thread per stage (identical in every wave)
