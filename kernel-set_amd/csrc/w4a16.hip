@@ -395,6 +395,58 @@ pipe_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
   }
 }
 
+// Split sum for the ring tile: ws[split][rows][n] in split order, + bias, -> C.
+// A workgroup takes 8 rows of one 128-column tile, a thread 4 adjacent
+// columns (16-byte loads; the ring path has N % 16 == 0). With tiles % 8 == 0
+// the pipe kernel ran every split of tile t on XCD t / (tiles / 8) (map_tile),
+// so workgroup id b (dispatched to XCD b % 8) takes a tile of that XCD and
+// reads the partials from the L2 they were written through.
+template <typename T>
+__global__ void __launch_bounds__(kThreads)
+pipe_reduce_kernel(uint16_t* __restrict__ c, const float* __restrict__ ws,
+                   const uint16_t* __restrict__ bias, int rows, int n, int splits, int tiles) {
+  const int rbs = (rows + 7) / 8;  // 8-row blocks per tile
+  int tile, rb;
+  if ((tiles & 7) == 0) {
+    const int i = blockIdx.x >> 3;
+    tile = (blockIdx.x & 7) * (tiles >> 3) + i / rbs;
+    rb = i % rbs;
+  } else {
+    tile = blockIdx.x / rbs;
+    rb = blockIdx.x % rbs;
+  }
+  const int row = 8 * rb + threadIdx.x / 32;
+  const int col = tile * w4pipe::kTileN + 4 * (threadIdx.x % 32);
+  if (row >= rows || col >= n) return;
+  const int64_t plane = static_cast<int64_t>(rows) * n;
+  const float* p = ws + static_cast<int64_t>(row) * n + col;
+  w4mma::f32x4 o = {0.f, 0.f, 0.f, 0.f};
+  int sp = 0;
+  for (; sp + 8 <= splits; sp += 8) {  // 8 loads in flight, added in order
+    w4mma::f32x4 part[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) part[i] = *reinterpret_cast<const w4mma::f32x4*>(p + (sp + i) * plane);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o += part[i];
+  }
+  if (sp < splits) {  // tail: clamped, guarded, still one batch in flight
+    w4mma::f32x4 part[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      part[i] = *reinterpret_cast<const w4mma::f32x4*>(p + min(sp + i, splits - 1) * plane);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (sp + i < splits) o += part[i];
+  }
+  uint16_t v[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = elem<T>::from_f32(bias ? o[e] + h2f<T>(bias[col + e]) : o[e]);
+  uint2 w;
+  w.x = v[0] | (static_cast<uint32_t>(v[1]) << 16);
+  w.y = v[2] | (static_cast<uint32_t>(v[3]) << 16);
+  *reinterpret_cast<uint2*>(c + static_cast<int64_t>(row) * n + col) = w;
+}
+
 template <typename T, int MB, bool OG>
 void launch_pipe_og(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_t* s,
                     const uint16_t* z, const uint16_t* bias, int64_t r0, int64_t r1, int64_t n,
@@ -455,7 +507,14 @@ ks_status_t run_pipe(uint16_t* c, const uint16_t* a, const uint8_t* b, const uin
       launch_pipe<T, 2>(c, a, b, s, z, bias, r0, r1, n, k, gs, tiles, splits, sps, sc.partial, st);
     else
       launch_pipe<T, 1>(c, a, b, s, z, bias, r0, r1, n, k, gs, tiles, splits, sps, sc.partial, st);
-    if (splits > 1) launch_reduce<T>(c + r0 * n, sc.partial, bias, r1 - r0, n, splits, st);
+    if (splits > 1 && !aligned(c, 8)) {
+      launch_reduce<T>(c + r0 * n, sc.partial, bias, r1 - r0, n, splits, st);
+    } else if (splits > 1) {  // 8-byte output stores (r0 * n is a multiple of 16)
+      const int rows = static_cast<int>(r1 - r0);
+      hipLaunchKernelGGL((pipe_reduce_kernel<T>), dim3(static_cast<unsigned>(tiles * ((rows + 7) / 8))),
+                         dim3(kThreads), 0, st, c + r0 * n, sc.partial, bias, rows,
+                         static_cast<int>(n), splits, tiles);
+    }
   }
   return KS_SUCCESS;
 }

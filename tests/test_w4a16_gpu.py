@@ -170,3 +170,28 @@ def test_batched_deterministic():
     o1, _ = run_w4a16(a, b, s, z, 128)
     o2, _ = run_w4a16(a, b, s, z, 128)
     assert np.array_equal(o1, o2)
+
+
+@pytest.mark.parametrize("m,n", [(16, 1024), (40, 1040), (64, 2048)])
+def test_ring_split_reduce_output_alignment(m, n):
+    """The ring tile's split reduce stores 4 outputs at a time when C is 8-byte
+    aligned and falls back to one output per thread otherwise; both sum the
+    splits in the same order, so C must be bit-identical, and within the
+    tolerance of the oracle (N = 1024: tiles % 8 == 0, XCD-mapped reduce;
+    N = 1040: 65 tiles, linear mapping)."""
+    k, gs = 4096, 128
+    a, codes, s, z = H.w4a16_inputs(m, k, n, gs, "int69", seed=m + n)
+    b = O.pack_k2_uint8(codes)
+    at, av = H.to_dev(a, "bf16")
+    st, sv = H.to_dev(s, "bf16")
+    zt, zv = H.to_dev(z, "bf16")
+    bt = H.np_u8_dev(b)
+    c0 = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+    ks.gemm.gemm_w4a16(c0, at, bt, st, zt, m, n, k, gs)
+    flat = torch.empty(m * n + 1, device="cuda", dtype=torch.bfloat16)
+    c1 = flat[1:].view(m, n)  # 2-byte aligned only
+    ks.gemm.gemm_w4a16(c1, at, bt, st, zt, m, n, k, gs)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(c0.view(torch.int16).cpu().numpy(), c1.view(torch.int16).cpu().numpy())
+    ref = O.w4a16_ref(av, b, sv, zv, gs, "bf16")
+    assert O.rel_err(H.from_dev_f32(c0), ref) <= TOL
