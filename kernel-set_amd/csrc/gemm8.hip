@@ -847,8 +847,7 @@ ks_status_t launch_fast_impl(Args p, hipStream_t s) {
   if (st != KS_SUCCESS) return st;
   p.ws = sc.partial;
   launch_fast_kernel<KIND, Out, UBS, true, BM>(p, tiles * p.splits, s);
-  hipLaunchKernelGGL((skinny::skinny_reduce_kernel<KIND, Out>),
-                     dim3(static_cast<unsigned>((p.m * p.n + 255) / 256)), dim3(256), 0, s, p);
+  skinny::launch_reduce<KIND, Out>(p, s);
   return KS_SUCCESS;
 }
 
@@ -904,8 +903,7 @@ ks_status_t launch_skinny(Args p, hipStream_t s, const char* who) {
   else
     hipLaunchKernelGGL((skinny::skinny_kernel<KIND, MB, CH, In, false>), dim3(grid),
                        dim3(skinny::kThreads), 0, s, p);
-  hipLaunchKernelGGL((skinny::skinny_reduce_kernel<KIND, Out>),
-                     dim3(static_cast<unsigned>((p.m * p.n + 255) / 256)), dim3(256), 0, s, p);
+  skinny::launch_reduce<KIND, Out>(p, s);
   return KS_SUCCESS;
 }
 
