@@ -4,8 +4,8 @@
 // Every operand moves global -> LDS directly (global_load_lds, no VGPRs
 // held) through a ring of D stages. Measured on MI355X (graph replay, cold,
 // K = 4096, N = 14336), two stages beat deeper rings at every pass height
-// (M = 16 / 32 / 64: 12.5 / 15.8 / 23.5 us against 15.0 / 16.9 / 24.2 us with
-// 6 / 4 / 3 stages; MoE config 5 gate_up 41 -> 37 us): a small ring lets more
+// (1024 cold calls: M = 16 / 64 16.5 / 25.8 -> 14.8 / 25.0 us against 6 / 3
+// stages; MoE config 5 gate_up 43.3 -> 40.1 us): a small ring lets more
 // workgroups share a CU (48-row MoE passes: three instead of two, so the
 // 768 (tile, expert) workgroups run in one round), and the other workgroups
 // on the CU hide the copy latency that one stage of prefetch leaves exposed.
