@@ -492,7 +492,7 @@ ks_status_t run_pipe(uint16_t* c, const uint16_t* a, const uint8_t* b, const uin
   sps = std::max(sps, std::min(total, 4));
   sps = ((sps + spg - 1) / spg) * spg;
   splits = (total + sps - 1) / sps;
-  const int64_t pass_rows = m > 32 ? 64 : (m > 16 ? 32 : 16);
+  const int64_t pass_rows = m > 48 ? 64 : (m > 32 ? 48 : (m > 16 ? 32 : 16));
   Scratch sc;
   if (splits > 1) {
     ks_status_t r = get_scratch(st, static_cast<size_t>(splits) * pass_rows * n, 0, &sc,
@@ -503,6 +503,8 @@ ks_status_t run_pipe(uint16_t* c, const uint16_t* a, const uint8_t* b, const uin
     const int64_t r1 = std::min(m, r0 + pass_rows);
     if (pass_rows == 64)
       launch_pipe<T, 4>(c, a, b, s, z, bias, r0, r1, n, k, gs, tiles, splits, sps, sc.partial, st);
+    else if (pass_rows == 48)
+      launch_pipe<T, 3>(c, a, b, s, z, bias, r0, r1, n, k, gs, tiles, splits, sps, sc.partial, st);
     else if (pass_rows == 32)
       launch_pipe<T, 2>(c, a, b, s, z, bias, r0, r1, n, k, gs, tiles, splits, sps, sc.partial, st);
     else

@@ -118,7 +118,7 @@ def test_config2_sweep(m):
     check(m, 4096, 14336, 128, zero_mode="int69", seed=100 + m)
 
 
-@pytest.mark.parametrize("m", [9, 16, 33, 64, 100, 257])
+@pytest.mark.parametrize("m", [9, 16, 33, 48, 64, 100, 257])
 @pytest.mark.parametrize("k,n,gs", [(1024, 384, 64), (2048, 272, 128), (4096, 512, 256),
                                     (1536, 256, 512), (960, 256, 64), (1024, 200, 32),
                                     (1024, 448, 128)])
