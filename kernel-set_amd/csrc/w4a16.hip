@@ -526,15 +526,16 @@ template <typename T, int BM, int BN>
 ks_status_t launch_dq(uint16_t* c, const uint16_t* a, const uint8_t* b, const uint16_t* s,
                const uint16_t* z, const uint16_t* bias, int64_t m, int64_t n, int64_t k, int gs,
                hipStream_t st) {
-  using C = w4dq::Cfg<BM, BN>;
-  // 128 x 128 tiles run the role-split kernel (w4a16_dqs.hpp), the others dq_kernel.
-  constexpr bool kSplitRoles = BM == 128 && BN == 128;
-  constexpr int kLds = kSplitRoles ? w4dqs::kBytes : C::kBytes;
+  using C = w4dq::Cfg<BM == 256 ? 128 : BM, BN>;
+  // 128 x 128 and 256 x 128 tiles run the role-split kernel (w4a16_dqs.hpp),
+  // the others dq_kernel.
+  constexpr bool kSplitRoles = BM >= 128 && BN == 128;
+  constexpr int kLds = kSplitRoles ? w4dqs::Geo<BM>::kBytes : C::kBytes;
   constexpr unsigned kBlock = kSplitRoles ? w4dqs::kThreads : C::kThreads;
   // opt in to the LDS size once per process (thread-safe static initialization)
   static const bool configured = [] {
     if constexpr (kSplitRoles)
-      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&w4dqs::dqs_kernel<T>),
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&w4dqs::dqs_kernel<T, BM>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
     else
       (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&w4dq::dq_kernel<T, BM, BN>),
@@ -568,7 +569,7 @@ ks_status_t launch_dq(uint16_t* c, const uint16_t* a, const uint8_t* b, const ui
   const dim3 grid(static_cast<unsigned>(n / BN), static_cast<unsigned>((m + BM - 1) / BM),
                   static_cast<unsigned>(splits));
   if constexpr (kSplitRoles)
-    hipLaunchKernelGGL((w4dqs::dqs_kernel<T>), grid, dim3(kBlock), kLds, st, c, a, b, s, z, bias, m,
+    hipLaunchKernelGGL((w4dqs::dqs_kernel<T, BM>), grid, dim3(kBlock), kLds, st, c, a, b, s, z, bias, m,
                        n, k, gs, sps, splits > 1 ? sc.partial : nullptr);
   else
     hipLaunchKernelGGL((w4dq::dq_kernel<T, BM, BN>), grid, dim3(kBlock), kLds, st, c, a, b, s, z,
@@ -749,6 +750,10 @@ ks_status_t run(void* c_, const void* a_, const void* b_, const void* s_, const 
     // 51 -> 43 us; N = 8192 M = 128 40.8 -> 30.7 us; N = 4096 M = 256
     // 40.4 -> 29.1 us, M = 65 24.9 -> 21.2 us; at 16 tiles, N = 2048 M = 96,
     // 16.5 -> 18.4 us, so smaller grids keep the 64-row tiles).
+    // 256 x 128 tiles (each weight dequantized once for 256 rows) when they
+    // alone give >= 192 workgroups: N = 14336 M = 512 / 1024 106 / 201 ->
+    // 95 / 180 us; with a K split instead (M = 256) they lost to 128 x 128.
+    if (m >= 384 && wide && wgs(256, 128) >= 192) return launch_dq<T, 256, 128>(c, a, b, s, z, bias, m, n, k, gs, st);
     if (m > 64 && wide && wgs(128, 128) >= 32) return launch_dq<T, 128, 128>(c, a, b, s, z, bias, m, n, k, gs, st);
     if (wide && wgs(64, 128) >= 192) return launch_dq<T, 64, 128>(c, a, b, s, z, bias, m, n, k, gs, st);
     if (m > 64 && wgs(128, 64) >= 192) return launch_dq<T, 128, 64>(c, a, b, s, z, bias, m, n, k, gs, st);

@@ -1,11 +1,21 @@
-// kernel-set (MI355X build) -- W4A16 GEMM for larger M, 128x128 tiles, with
-// the waves split by role (warp specialization):
+// kernel-set (MI355X build) -- W4A16 GEMM for larger M, 128x128 or 256x128
+// tiles, with the waves split by role (warp specialization):
 //
 //  * waves 4-7 (producers, one per SIMD) copy the operands global -> LDS
 //    through a kDepth-stage ring (direct copies, no VGPRs) and dequantize
 //    the next stage's weights into the bf16/f16 tile Wd [128 n][64 k];
 //  * waves 0-3 (consumers, one per SIMD) run the 32x32x16 MFMAs of a 64x64
-//    output tile each on the current stage's A and Wd.
+//    (128-row tile) or 128x64 (256-row tile) output tile each on the current
+//    stage's A and Wd.
+//
+// The two roles run separate loops that pass the same per-stage barriers, so
+// the consumers' accumulators are not live across the producers' code (one
+// shared loop held 174 VGPRs for the 128-row tile and spilled for the 256-row
+// one; now 112 / 208, and the 128-row tile measured 5-10 % faster, e.g. M =
+// 256 N = 14336 K = 4096 62 -> 56 us). The 256-row tile dequantizes each
+// weight once for twice the rows; it serves M >= 384 when it alone fills 192
+// workgroups (N = 14336 M = 512 / 1024: 106 / 201 -> 95 / 180 us); with a
+// K split (M = 256) it was slower than the 128-row tile (63 against 56 us).
 //
 // Both roles work on different stages between the same per-stage barrier, so
 // a stage costs max(copy + dequantize, MFMA) instead of their sum. Every
@@ -45,35 +55,45 @@ using w4dq::lds_i32x2;
 using w4dq::wait_lgkm0;
 using w4dq::wait_vmcnt;
 
-constexpr int kBM = 128, kBN = 128;
+constexpr int kBN = 128;
 constexpr int kThreads = 512;
-constexpr int kDepth = 4;
-constexpr int kABytes = kBM * kStageK * 2;      // A [128 rows][64 k]: 16 KB
 constexpr int kWBytes = (kStageK / 2) * kBN;    // raw packed rows of a stage: 4 KB
 constexpr int kSzBytes = 2 * kBN * 2;           // one producer's scales + zeros
-constexpr int kSlot = kABytes + kWBytes + 4 * kSzBytes;
 constexpr int kWdBytes = kBN * kStageK * 2;     // Wd [128 n][64 k]: 16 KB
-constexpr int kBytes = kSlot * kDepth + 2 * kWdBytes;
-constexpr int kLoads = 4 + 1 + 2;               // copies per producer per stage
-static_assert(kBytes <= 160 * 1024, "LDS");
 
-// Rows [m0, m0+128) (clamped reads at row_end-1, outputs past row_end dropped)
+// Tile height BM = 128 or 256 rows (256: each consumer wave owns 128 x 64 and
+// the tile copies half the activation bytes per MFMA of the 128-row tile).
+template <int BM>
+struct Geo {
+  static constexpr int kABytes = BM * kStageK * 2;     // A [BM rows][64 k]: 16 / 32 KB
+  static constexpr int kSlot = kABytes + kWBytes + 4 * kSzBytes;
+  static constexpr int kDepth = BM == 128 ? 4 : 3;  // 4 x 21.5 / 3 x 37.5 KB + Wd
+  static constexpr int kBytes = kSlot * kDepth + 2 * kWdBytes;
+  static constexpr int kACopies = BM / 32;             // A copies per producer per stage
+  static constexpr int kLoads = kACopies + 1 + 2;      // copies per producer per stage
+  static constexpr int kRB = BM / 64;                  // 32-row MFMA blocks per consumer
+  static_assert(kBytes <= 160 * 1024, "LDS");
+};
+
+// Rows [m0, m0+BM) (clamped reads at row_end-1, outputs past row_end dropped)
 // x columns [n0, n0+128), K stages [st0, st0 + sps) of grid z. Requires
 // K % 64 == 0, gs % 64 == 0, N % 128 == 0, 16-byte aligned a and b, 4-byte
 // aligned scales and zeros; sps a multiple of gs / 64.
-template <typename T>
+template <typename T, int BM>
 __global__ void __launch_bounds__(kThreads)
 dqs_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
            const uint8_t* __restrict__ b, const uint16_t* __restrict__ scales,
            const uint16_t* __restrict__ zeros, const uint16_t* __restrict__ bias,
            int64_t row_end, int64_t n, int64_t k, int gs, int sps, float* __restrict__ ws) {
-  constexpr int D = kDepth;
+  using G = Geo<BM>;
+  constexpr int D = G::kDepth, kSlot = G::kSlot, kABytes = G::kABytes, kLoads = G::kLoads;
+  constexpr int kAC = G::kACopies, kRB = G::kRB;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   uint8_t* ring = smem;
   uint8_t* wd = smem + kSlot * D;  // [2][128 n][128 B]
 
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kBN;
-  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kBM;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * BM;
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
   const bool producer = wave >= 4;
@@ -83,10 +103,10 @@ dqs_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
 
   // ---- producer state (wave p = wave - 4) ----
   const int p = wave & 3;
-  const uint16_t* a_cur[4];
+  const uint16_t* a_cur[kAC];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {  // A copy 4p + i: rows 8(4p+i) .. +7, one 128-B row per 8 lanes
-    const int row = 8 * (4 * p + i) + lane / 8;
+  for (int i = 0; i < kAC; ++i) {  // A copy kAC*p + i: rows 8(kAC*p+i) .. +7, one 128-B row per 8 lanes
+    const int row = 8 * (kAC * p + i) + lane / 8;
     const int cc = (lane % 8) ^ (row & 7);
     const int64_t gr = min<int64_t>(m0 + row, row_end - 1);
     a_cur[i] = a + gr * k + static_cast<int64_t>(st0) * kStageK + 8 * cc;
@@ -102,8 +122,8 @@ dqs_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
   auto issue = [&]() {
     uint8_t* slot = ring + is_slot * kSlot;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      dma_to_lds<16>(a_cur[i], slot + 1024 * (4 * p + i));
+    for (int i = 0; i < kAC; ++i) {
+      dma_to_lds<16>(a_cur[i], slot + 1024 * (kAC * p + i));
       a_cur[i] += kStageK;
     }
     dma_to_lds<16>(w_cur, slot + kABytes + 1024 * p);
@@ -151,28 +171,19 @@ dqs_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
     }
   };
 
-  // ---- consumer state: wave (wr, wc) -> rows 64 wr .., columns 64 wc .. ----
-  const int cm = (wave >> 1) * 64, cn = (wave & 1) * 64;
-  const int l32 = lane % 32, lh = lane / 32;
-  f32x16 acc[2][2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
-
   if (producer) {
+    // The producers' loop is separate from the consumers', so the
+    // accumulators are not live across the dequantization (both loops pass
+    // the same barriers, one per stage).
 #pragma unroll 1
     for (int i = 0; i < D - 1 && i < nst; ++i) issue();
     if (nst >= D - 1) wait_vmcnt<(D - 2) * kLoads>();
     else wait_vmcnt<0>();
     dequant(ring, wd);
     wait_lgkm0();
-  }
-  barrier_no_wait();  // stage 0: A landed, Wd[0] written
-
+    barrier_no_wait();  // stage 0: A landed, Wd[0] written
 #pragma unroll 1
-  for (int st = 0; st < nst; ++st) {
-    if (producer) {
+    for (int st = 0; st < nst; ++st) {
       // Slot (st + D - 1) % D held stage st - 1, which the consumers finished
       // before the last barrier; Wd[(st + 1) & 1] likewise.
       const bool more = st + D - 1 < nst;
@@ -184,29 +195,46 @@ dqs_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
         dequant(ring + nx * kSlot, wd + ((st + 1) & 1) * kWdBytes);
         wait_lgkm0();
       }
-    } else {
-      const uint8_t* as = ring + (st % D) * kSlot;
-      const uint8_t* bs = wd + (st & 1) * kWdBytes;
+      barrier_no_wait();  // stage st consumed; stage st + 1's A and Wd published
+    }
+    return;
+  }
+
+  // ---- consumer state: wave (wr, wc) -> rows BM/2 wr .., columns 64 wc .. ----
+  const int cm = (wave >> 1) * (BM / 2), cn = (wave & 1) * 64;
+  const int l32 = lane % 32, lh = lane / 32;
+  f32x16 acc[kRB][2];
 #pragma unroll
-      for (int ks = 0; ks < kStageK / 16; ++ks) {
-        const int chunk = 2 * ks + lh;  // 8 k per lane: k = 16ks + 8lh .. +7
-        uint4 af[2], bf[2];
+  for (int i = 0; i < kRB; ++i)
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          const int am = cm + 32 * i + l32;
-          af[i] = *reinterpret_cast<const uint4*>(as + am * 128 + ((chunk ^ (am & 7)) * 16));
-          const int bn = cn + 32 * i + l32;
-          bf[i] = *reinterpret_cast<const uint4*>(bs + bn * 128 + ((chunk ^ (bn & 7)) * 16));
-        }
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+  barrier_no_wait();  // stage 0 published
+
+#pragma unroll 1
+  for (int st = 0; st < nst; ++st) {
+    const uint8_t* as = ring + (st % D) * kSlot;
+    const uint8_t* bs = wd + (st & 1) * kWdBytes;
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+    for (int ks = 0; ks < kStageK / 16; ++ks) {
+      const int chunk = 2 * ks + lh;  // 8 k per lane: k = 16ks + 8lh .. +7
+      uint4 af[kRB], bf[2];
 #pragma unroll
-          for (int j = 0; j < 2; ++j) acc[i][j] = dq_traits<T>::mma(af[i], bf[j], acc[i][j]);
+      for (int i = 0; i < kRB; ++i) {
+        const int am = cm + 32 * i + l32;
+        af[i] = *reinterpret_cast<const uint4*>(as + am * 128 + ((chunk ^ (am & 7)) * 16));
       }
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int bn = cn + 32 * i + l32;
+        bf[i] = *reinterpret_cast<const uint4*>(bs + bn * 128 + ((chunk ^ (bn & 7)) * 16));
+      }
+#pragma unroll
+      for (int i = 0; i < kRB; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = dq_traits<T>::mma(af[i], bf[j], acc[i][j]);
     }
     barrier_no_wait();  // stage st consumed; stage st + 1's A and Wd published
   }
-  if (producer) return;
 
   // ---- epilogue: acc[i][j][r] -> row 8*(r/4) + 4*lh + r%4 of 32x32 tile (i, j) ----
 #pragma unroll
@@ -214,7 +242,7 @@ dqs_kernel(uint16_t* __restrict__ c, const uint16_t* __restrict__ a,
     const int64_t col = n0 + cn + 32 * j + l32;
     const float bv = (bias && !ws) ? elem<T>::to_f32(bias[col]) : 0.f;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < kRB; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int64_t row = m0 + cm + 32 * i + 8 * (r / 4) + 4 * lh + (r % 4);

@@ -156,10 +156,13 @@ def test_dq_split_k(dt):
     (70, 2048, 14336, 64, None, "f16", False),
     (65, 1024, 4096, 128, "int69", "bf16", True),   # 32 tiles
     (200, 2048, 4096, 64, None, "f16", False),      # 64 tiles
+    # M >= 384 with >= 192 tiles of 256 x 128: the 256-row role-split tile
+    (400, 512, 24576, 128, "int69", "bf16", True),
+    (512, 512, 12288, 64, None, "f16", False),
 ])
 def test_dq_role_split_tiles(m, k, n, gs, zero_mode, dt, bias):
-    # M > 64 with >= 32 tiles of 128 x 128 (K split below 192 workgroups): the
-    # role-split kernel (producer waves copy and dequantize, consumer waves run
+    # M > 64 with >= 32 tiles of 128 x 128 (K split below 192 workgroups), or
+    # M >= 384 with >= 192 tiles of 256 x 128: the role-split kernel (producer waves copy and dequantize, consumer waves run
     # the MFMAs); M not a multiple of 128 leaves a ragged last row tile.
     check(m, k, n, gs, zero_mode=zero_mode, dt=dt, seed=m + gs, bias=bias)
 
