@@ -553,6 +553,11 @@ ks_status_t launch_dq(uint16_t* c, const uint16_t* a, const uint8_t* b, const ui
   int splits = 1, sps = nst;
   if (wgs < 192) {
     splits = static_cast<int>(std::min<int64_t>((224 + wgs - 1) / wgs, nst / (2 * spg)));
+    // The role-split kernel holds one workgroup per CU: more than 256
+    // workgroups would leave a second, mostly idle round (N = 4096 M = 384:
+    // 96 tiles x 3 splits took 46 us, longer than M = 512's 2 x 128).
+    if constexpr (kSplitRoles)
+      while (splits > 1 && wgs * splits > 256) --splits;
     if (splits > 1) {
       sps = ((nst + splits - 1) / splits + spg - 1) / spg * spg;
       splits = (nst + sps - 1) / sps;
