@@ -195,16 +195,31 @@ __device__ inline void pipe_tile(const PipeArgs& p, int64_t r0, int64_t r_end, i
   // Promotion with the scale/zero slot pair `half` (0: first 64 k, 1: last);
   // leaves P and S cleared for the next group (OG: the next stage's first
   // MFMAs overwrite them instead).
-  auto promote = [&](const uint8_t* szl, int half) {
+  // The promotion's per-column factors of scale/zero slot pair `half`: read
+  // at the stage start (their LDS latency then hides under the MFMAs), both
+  // values read unconditionally (the zero slot holds scales when there are
+  // no zeros) and selected, so no branch splits the stage.
+  struct Fac { float se[2], cz[2]; };
+  auto factors = [&](const uint8_t* szl, int half) {
     const uint16_t* sl = reinterpret_cast<const uint16_t*>(szl + 512 * half);
     const uint16_t* zl = reinterpret_cast<const uint16_t*>(szl + 512 * half + 256);
+    Fac f;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int cc = 32 * wave + 16 * j + li;
       const float sc = elem<T>::to_f32(sl[cc]);
-      const float zz = has_z ? elem<T>::to_f32(zl[cc]) : 0.f;
-      const float cz = 128.0f + zz * unit;
-      const float se = sc * inv_unit;
+      const float zr = elem<T>::to_f32(zl[cc]);
+      const float zz = has_z ? zr : 0.f;
+      f.cz[j] = 128.0f + zz * unit;
+      f.se[j] = sc * inv_unit;
+    }
+    return f;
+  };
+  auto promote = [&](const Fac& f) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const float cz = f.cz[j];
+      const float se = f.se[j];
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
@@ -233,6 +248,9 @@ __device__ inline void pipe_tile(const PipeArgs& p, int64_t r0, int64_t r_end, i
     slot_i = (slot_i + 1 == D) ? 0 : slot_i + 1;
     const uint8_t* al = slot + kWBytes;
     const uint8_t* szl = slot + kWBytes + R::kABytes;
+    const Fac f0 = factors(szl, 0);
+    Fac f1 = f0;
+    if (half_groups) f1 = factors(szl, 1);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const uint8_t* wl = slot + (32 * h + tr_row) * 128;
@@ -259,14 +277,14 @@ __device__ inline void pipe_tile(const PipeArgs& p, int64_t r0, int64_t r_end, i
           S[mb] = w4mma::mfma_traits<T>::mma(af, ones, fresh ? zero4 : S[mb]);
         }
       }
-      if (!OG && half_groups) promote(szl, h);
+      if (!OG && half_groups) promote(h == 0 ? f0 : f1);
     }
     if constexpr (OG) {
-      promote(szl, 0);
+      promote(f0);
     } else if (!half_groups) {
       if (++grp_pos == sps || i == nst - 1) {
         grp_pos = 0;
-        promote(szl, 0);
+        promote(f0);
       }
     }
   }
