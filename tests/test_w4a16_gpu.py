@@ -198,3 +198,20 @@ def test_ring_split_reduce_output_alignment(m, n):
     np.testing.assert_array_equal(c0.view(torch.int16).cpu().numpy(), c1.view(torch.int16).cpu().numpy())
     ref = O.w4a16_ref(av, b, sv, zv, gs, "bf16")
     assert O.rel_err(H.from_dev_f32(c0), ref) <= TOL
+
+
+def test_dq_256_row_tile_matches_128_row_tile():
+    # N = 14336, M = 512 runs the 256 x 128 role-split tile and M = 256 the
+    # 128 x 128 one, neither with a K split. Both accumulate each output over
+    # the same 64-k stages and 16-k MFMA slices in the same order, so the
+    # first 256 rows must agree bit for bit; the rows of the second tile are
+    # checked against the oracle on a sample.
+    m, k, n, gs = 512, 4096, 14336, 128
+    a, codes, s, z = H.w4a16_inputs(m, k, n, gs, "int69", seed=512)
+    b = O.pack_k2_uint8(codes)
+    out, (av, sv, zv, _) = run_w4a16(a, b, s, z, gs)
+    out256, _ = run_w4a16(a[:256], b, s, z, gs)
+    assert np.array_equal(out[:256], out256)
+    rows = np.array([0, 255, 256, 300, 383, 384, 511])
+    ref = O.w4a16_ref(av[rows], b, sv, zv, gs, "bf16")
+    assert O.rel_err(out[rows], ref) <= TOL
