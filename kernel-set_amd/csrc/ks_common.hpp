@@ -87,12 +87,16 @@ __device__ inline float bf16_bits_to_f32(uint16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }
 
-// fp32 -> bf16, round to nearest even; NaN stays a quiet NaN.
+// fp32 -> bf16, round to nearest even; NaN stays a quiet NaN (its top 16 bits
+// with the quiet bit set). gfx950 converts in hardware (v_cvt_pk_bf16_f32);
+// checked on MI355X against the integer form
+//   NaN: (u >> 16) | 0x40, else (u + 0x7fff + ((u >> 16) & 1)) >> 16
+// for all 2^32 inputs, with no difference.
 __device__ inline uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x0040u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  const __bf16 b = static_cast<__bf16>(f);
+  uint16_t u;
+  __builtin_memcpy(&u, &b, 2);
+  return u;
 }
 
 __device__ inline float f16_bits_to_f32(uint16_t h) {
