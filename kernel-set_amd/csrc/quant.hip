@@ -17,6 +17,7 @@
 #include <type_traits>
 
 #include "kernel_set/quant.h"
+#include "kernel_set/testing.h"
 #include "ks_common.hpp"
 
 namespace ks {
@@ -572,6 +573,16 @@ struct DequantInt4Op {
   }
 };
 
+// out[i] = the 16-bit output rounding every kernel applies (elem<Out>::from_f32)
+// to the fp32 bit pattern start + i (test hook: no input buffer needed).
+template <typename Out>
+__global__ void __launch_bounds__(kThreads)
+round_bits_kernel(uint16_t* __restrict__ out, uint32_t start, int64_t n) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * kThreads)
+    out[i] = elem<Out>::from_f32(__uint_as_float(start + static_cast<uint32_t>(i)));
+}
+
 }  // namespace quant
 }  // namespace ks
 
@@ -752,6 +763,25 @@ ks_status_t ks_repack_int4(void* out_packed, const void* qweight, const void* pe
                        static_cast<uint8_t*>(out_packed), static_cast<const uint32_t*>(qweight),
                        static_cast<const int32_t*>(perm), size_k, size_n);
   KS_LAUNCH_STATUS("ks_repack_int4");
+  return KS_SUCCESS;
+}
+
+ks_status_t ks_testing_round_bits(void* out, uint32_t start, int64_t n, ks_dtype_t out_dtype,
+                                  ks_stream_t stream) {
+  KS_REQUIRE_PTR(out);
+  if (n <= 0 || n > (int64_t{1} << 32) - start)
+    KS_FAIL(KS_ERROR_INVALID_ARGUMENT, "ks_testing_round_bits: bad range");
+  auto s = to_stream(stream);
+  const unsigned g = stride_grid(n);
+  if (out_dtype == KS_DTYPE_BF16)
+    hipLaunchKernelGGL((round_bits_kernel<bf16_t>), dim3(g), dim3(kThreads), 0, s,
+                       static_cast<uint16_t*>(out), start, n);
+  else if (out_dtype == KS_DTYPE_F16)
+    hipLaunchKernelGGL((round_bits_kernel<f16_t>), dim3(g), dim3(kThreads), 0, s,
+                       static_cast<uint16_t*>(out), start, n);
+  else
+    KS_FAIL(KS_ERROR_UNSUPPORTED_DTYPE, "ks_testing_round_bits: out_dtype must be bf16 or f16");
+  KS_LAUNCH_STATUS("ks_testing_round_bits");
   return KS_SUCCESS;
 }
 

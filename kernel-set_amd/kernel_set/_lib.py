@@ -176,6 +176,7 @@ _decl("ks_moe_grouped_gemm_w4a16",
       [_VP, _VP, _VP, _VP, _VP, _I32P, _I, _I64, _I64, _I64, _I, _I, _VP])
 # testing.h (test hook, not reference ABI)
 _decl("ks_testing_gemm_w8a8_i32", [_I32P, _VP, _VP, _I64, _I64, _I64, _VP])
+_decl("ks_testing_round_bits", [_VP, ctypes.c_uint32, _I64, _I, _VP])
 
 
 def status_string(status: int) -> str:

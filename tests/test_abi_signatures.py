@@ -85,7 +85,7 @@ def test_a_prototype_edit_is_detected(tmp_path, edit):
 
 _C_TO_CTYPES = {
     "void*": ctypes.c_void_p, "const void*": ctypes.c_void_p, "ks_stream_t": ctypes.c_void_p,
-    "int64_t": ctypes.c_int64, "int": ctypes.c_int, "ks_dtype_t": ctypes.c_int,
+    "int64_t": ctypes.c_int64, "uint32_t": ctypes.c_uint32, "int": ctypes.c_int, "ks_dtype_t": ctypes.c_int,
     "ks_quant_mode_t": ctypes.c_int, "ks_memcpy_kind_t": ctypes.c_int,
     "ks_status_t": ctypes.c_int, "size_t": ctypes.c_size_t, "float": ctypes.c_float,
     "const char*": ctypes.c_char_p,
