@@ -451,6 +451,18 @@ gemm8_fast_kernel(Args p) {
   // B transposed-read addressing: lane (2*jj + h) of its 16-lane group reads
   // k-row (kbase + jj), bytes 8h..8h+7 of the 16-column block.
   const int tr_jj = li >> 1, tr_h = li & 1;
+  // Every transposed read of a step is at k-row 16*lk + c + tr_jj for a
+  // constant c in {0, 8, 64, 72}, and b_swz gives the same chunk for all four
+  // (row & 7 == tr_jj, and bit 3 depends only on lk), so the lane's byte
+  // offset within a buffer is b_lane[j] + c * kFBRow: fixed per lane for the
+  // whole K loop, with c folded into the reads' immediate offsets.
+  uint32_t b_lane[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int row0 = 16 * lk + tr_jj;
+    b_lane[j] = static_cast<uint32_t>(row0 * kFBRow +
+                                      ((((wn + 16 * j) >> 4) ^ b_swz(row0)) * 16) + 8 * tr_h);
+  }
 
   // fp8: the last two partials of a step are promoted at the start of the next.
   f32x4 plast[2], sclast;
@@ -484,11 +496,9 @@ gemm8_fast_kernel(Args p) {
     const uint8_t* a_src = sA + cur * BM * kFARow;
     const uint8_t* b_src = sB + cur * kBK * kFBRow;
 
-    // B fragment of n-block j: k rows kb0 + 0..KLEN-1 of columns wn+16j..+15
-    auto b_tr8 = [&](int j, int krow) -> i32x2 {
-      const int row = krow + tr_jj;
-      const int chunk = ((wn + 16 * j) >> 4) ^ b_swz(row);
-      const uint8_t* addr = b_src + row * kFBRow + chunk * 16 + 8 * tr_h;
+    // B fragment of n-block j: k rows 16*lk + c + (0..7) of columns wn+16j..+15
+    auto b_tr8 = [&](int j, int c) -> i32x2 {
+      const uint8_t* addr = b_src + b_lane[j] + c * kFBRow;
       return __builtin_amdgcn_ds_read_tr8_b64_v2i32(reinterpret_cast<lds_i32x2*>(
           reinterpret_cast<uintptr_t>(addr)));
     };
@@ -521,8 +531,8 @@ gemm8_fast_kernel(Args p) {
       float bs[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const i32x2 q0 = b_tr8(j, 16 * lk + 0), q1 = b_tr8(j, 16 * lk + 8);
-        const i32x2 q2 = b_tr8(j, 64 + 16 * lk), q3 = b_tr8(j, 64 + 16 * lk + 8);
+        const i32x2 q0 = b_tr8(j, 0), q1 = b_tr8(j, 8);
+        const i32x2 q2 = b_tr8(j, 64), q3 = b_tr8(j, 72);
         fb[j] = i32x8{q0[0], q0[1], q1[0], q1[1], q2[0], q2[1], q3[0], q3[1]};
         bs[j] = sBs[cur * kFBN + wn + 16 * j + li];
       }
@@ -569,8 +579,8 @@ gemm8_fast_kernel(Args p) {
       i32x8 fbp[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const i32x2 q0 = b_tr8(j, 16 * lk + 0), q1 = b_tr8(j, 16 * lk + 8);
-        const i32x2 q2 = b_tr8(j, 64 + 16 * lk), q3 = b_tr8(j, 64 + 16 * lk + 8);
+        const i32x2 q0 = b_tr8(j, 0), q1 = b_tr8(j, 8);
+        const i32x2 q2 = b_tr8(j, 64), q3 = b_tr8(j, 72);
         fbp[j] = i32x8{q0[0], q0[1], q1[0], q1[1], q2[0], q2[1], q3[0], q3[1]};
       }
 #pragma unroll
@@ -600,7 +610,7 @@ gemm8_fast_kernel(Args p) {
         i32x4 fb[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const i32x2 q0 = b_tr8(j, 64 * h + 16 * lk), q1 = b_tr8(j, 64 * h + 16 * lk + 8);
+          const i32x2 q0 = b_tr8(j, 64 * h), q1 = b_tr8(j, 64 * h + 8);
           fb[j] = i32x4{q0[0], q0[1], q1[0], q1[1]};
         }
 #pragma unroll
